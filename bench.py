@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention block: fwd+bwd tokens/s and peak HBM on one GPU.
+
+Workload: the 50M-pretrain block shape B=64, T=4096, C=512, H=8, N=64, bf16
+(262,144 tokens per step), synthetic seeded inputs resident in HBM before
+the timed region. A step is one forward and one backward of
+FusedAttentionFunction over the whole batch (input and all five weight
+gradients; the rotary tables are buffers, as in a YaRN module).
+
+Printed on stdout: ONE JSON line with the metric, the per-kernel roofline of
+the dominant kernel (timed live with HIP events on its launch stream over the
+timed region), peak HBM, and the CPU baseline (the fp32 oracle on a bounded
+batch slice on the host cores). Progress goes to stderr.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--compare-eager] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+METRIC = "fwd+bwd tokens/s & peak mem, attn block bf16 B64 T4096 C512 H8 N64"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+ROOT = Path(__file__).resolve().parent
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def kernel_work(w):
+    """Algorithmic flops and bytes per launch of each kernel.
+    Attention pairs are counted exactly (causal T(T+1)/2); a product that a
+    kernel recomputes (S in both backward kernels, dP in the dQ kernel) is
+    not algorithmic work and is not counted."""
+    B, T, C, H, N = w.B, w.T, w.C, w.H, w.N
+    M, HN = B * T, H * N
+    pair = 2.0 * B * H * N * T * (T + 1) / 2  # flops of one causal (T x T x N) product
+    return {
+        "qkvg_proj": dict(flops=2.0 * M * C * 4 * HN, bytes=2.0 * M * C + 2.0 * 4 * M * HN),
+        "attn_fwd": dict(flops=2 * pair, bytes=2.0 * 4 * M * HN),
+        "gate_oproj": dict(flops=2.0 * M * HN * C, bytes=2.0 * 2 * M * HN + 2.0 * M * C),
+        "dz_gate_bwd": dict(flops=2.0 * M * C * HN, bytes=2.0 * M * C + 2.0 * 4 * M * HN),
+        "attn_bwd_dq": dict(flops=1 * pair, bytes=2.0 * 3 * M * HN),
+        "attn_bwd_dkdv": dict(flops=3 * pair, bytes=2.0 * 6 * M * HN),
+        "dw_partial": dict(flops=2.0 * M * (4 * HN * C + C * HN), bytes=2.0 * M * (4 * HN + C + C + 2 * HN)),
+        "dx": dict(flops=2.0 * M * 4 * HN * C, bytes=2.0 * M * (4 * HN + 2 * C)),
+    }
+
+
+def cpu_baseline(w, seconds: float):
+    """The fp32 oracle (eager block, CPU) on a batch slice of the workload."""
+    import torch
+
+    from memory_efficient_attn_layer_amd.synthetic import make_inputs
+    from oracle import block as ob
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = max(1, min(threads, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    inp = make_inputs(w, B=1, dtype=torch.float32)
+    ob.block_grads(inp, w.H, w.N, dtype=torch.float32)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < seconds and len(times) < 20):
+        t0 = time.perf_counter()
+        ob.block_grads(inp, w.H, w.N, dtype=torch.float32)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 3 * seconds:
+            break
+    med = statistics.median(times)
+    return {
+        "value": w.T / med,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"fp32 oracle fwd+bwd (oracle/block.py) on 1 of {w.B} sequences (T={w.T}, C={w.C}, "
+                  f"H={w.H}, N={w.N}); 1 warm-up + {len(times)} timed iterations, median {med:.2f} s",
+    }
+
+
+def eager_block(x, wq, wk, wv, wg, wo, f1, f2, H, N):
+    """The reference's eager path on the GPU (README.md:42-64): checkpointed
+    projections + SDPA flash + gate + o_proj, in bf16."""
+    import torch
+    import torch.nn.functional as F
+    from torch.utils.checkpoint import checkpoint
+
+    from memory_efficient_attn_layer_amd.yarn import swap_even_odd
+
+    B, T, C = x.shape
+    fs1, fs2 = f1[:T, None, :], f2[:T, None, :]
+
+    def forward1(x):
+        x = F.rms_norm(x, (C,), eps=1e-6)
+        q = F.linear(x, wq).view(B, T, H, N)
+        k = F.linear(x, wk).view(B, T, H, N)
+        v = F.linear(x, wv).view(B, T, H, N)
+        g = F.linear(x, wg)
+        q = F.rms_norm(q, (N,), eps=1e-6)
+        k = F.rms_norm(k, (N,), eps=1e-6)
+        q = q * fs1 + swap_even_odd(q) * fs2
+        k = k * fs1 + swap_even_odd(k) * fs2
+        return q, k, v, g
+
+    q, k, v, g = checkpoint(forward1, x, use_reentrant=False)
+    with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.FLASH_ATTENTION):
+        o = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                           is_causal=True).transpose(1, 2).contiguous().view(B, T, H * N)
+    return F.linear(o * torch.sigmoid(g), wo)
+
+
+def measure(step, steps, warmup, sync):
+    for _ in range(warmup):
+        step()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    sync()
+    return (time.perf_counter() - t0) / steps
+
+
+def peak_of(step, sync):
+    import torch
+
+    sync()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    step()
+    sync()
+    return torch.cuda.max_memory_allocated() - base
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", type=int, default=1, help="workload id (1 = the north-star shape)")
+    ap.add_argument("--compare-eager", action="store_true", help="also time the eager SDPA path on the GPU")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported; this block runs on one GPU only "
+              "(no collective or sharded path is built). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from memory_efficient_attn_layer_amd import _lib
+    from memory_efficient_attn_layer_amd.attention import FusedAttentionFunction
+    from memory_efficient_attn_layer_amd.synthetic import WORKLOADS, make_inputs
+
+    w = WORKLOADS[args.workload]
+    if not w.backward:
+        raise SystemExit(f"workload {args.workload} is forward-only; bench.py measures fwd+bwd")
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"workload {w.name}; generating inputs")
+    inp = make_inputs(w, device=dev)
+    x = inp["x"].requires_grad_(True)
+    ws = [inp[n].requires_grad_(True) for n in ("wq", "wk", "wv", "wg", "wo")]
+    f1, f2, dy = inp["f1"], inp["f2"], inp["dy"]
+    H, N = w.H, w.N
+    sync = torch.cuda.synchronize
+
+    def step():
+        y = FusedAttentionFunction.apply(x, *ws, f1, f2, H, N, 1e-6)
+        return torch.autograd.grad(y, [x, *ws], dy)
+
+    log("warm-up")
+    for _ in range(max(1, args.warmup)):
+        step()
+    sync()
+    peak = peak_of(step, sync)
+    log(f"peak HBM over one step: {peak / 2**20:.1f} MiB")
+
+    _lib.profile_enable(True)
+    sec = measure(step, args.steps, 0, sync)
+    _lib.profile_enable(False)
+    prof = _lib.profile_read()
+    ms = sec * 1e3
+    tokens = w.B * w.T
+    log(f"{ms:.3f} ms/step, {tokens / sec / 1e6:.2f} M tokens/s")
+
+    work = kernel_work(w)
+    kernels = {}
+    for name, (cnt, tot) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        avg = tot / cnt
+        ent = {"launches_per_step": cnt / args.steps, "avg_ms": round(avg, 4), "share": round(tot / (ms * args.steps), 4)}
+        if name in work:
+            ent["tflops"] = round(work[name]["flops"] / (avg * 1e-3) / 1e12, 2)
+            ent["gbs"] = round(work[name]["bytes"] / (avg * 1e-3) / 1e9, 1)
+        kernels[name] = ent
+        log(f"  {name:15s} {avg:8.4f} ms x{cnt / args.steps:.0f}  {ent.get('tflops', '-')} TFLOP/s")
+    dom = max((k for k in prof if k in work), key=lambda k: prof[k][1])
+    avg_s = prof[dom][1] / prof[dom][0] * 1e-3
+    achieved = work[dom]["flops"] / avg_s / 1e12
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get(dom)
+        except (ValueError, OSError):
+            traffic = None
+    roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
+
+    eager = None
+    if args.compare_eager:
+        log("eager SDPA comparator")
+        try:
+            def estep():
+                y = eager_block(x, *ws, f1, f2, H, N)
+                return torch.autograd.grad(y, [x, *ws], dy)
+
+            epeak = peak_of(estep, sync)
+            esec = measure(estep, max(3, args.steps // 4), 2, sync)
+            eager = {"tokens_per_s": round(tokens / esec, 1), "ms_per_step": round(esec * 1e3, 3),
+                     "peak_hbm_bytes": int(epeak)}
+            log(f"eager: {esec * 1e3:.3f} ms/step, peak {epeak / 2**20:.1f} MiB")
+        except Exception as e:  # noqa: BLE001 - report, do not fail the benchmark
+            eager = {"error": f"{type(e).__name__}: {e}"[:300]}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (fp32 oracle)")
+        cpu = cpu_baseline(w, args.cpu_seconds)
+        log(f"cpu: {cpu['value']:.1f} tokens/s on {cpu['cores']} cores")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tokens / sec, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": w.name, "B": w.B, "T": w.T, "C": w.C, "H": H, "N": N,
+                   "tokens_per_step": tokens, "parallelism": "single-gpu"},
+        "peak_hbm": {"fused_bytes": int(peak), "eager_sdpa": eager},
+        "block_tflops": round(3 * w.flops_fwd() / sec / 1e12, 2),
+        "roofline": roofline,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

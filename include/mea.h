@@ -1,0 +1,183 @@
+/*
+ * mea.h - C ABI of the MI355X (gfx950) memory-efficient attention block.
+ *
+ * The block is the one computed by `fused_attn` in the reference
+ * (fast_triton_attn.py:681-697) and by the eager path it replaces
+ * (README.md:42-64):
+ *
+ *   xh = rmsnorm(x)                              per token over C
+ *   a_p = xh W_p^T             p in {q,k,v,g}    W_p is (H*N, C)
+ *   q = rope(rmsnorm_N(a_q)), k = rope(rmsnorm_N(a_k)), v = a_v, s = sigmoid(a_g)
+ *   O = softmax_causal(q k^T / sqrt(N)) v        per (batch, head)
+ *   y = (O * s) W_o^T                            W_o is (C, H*N)
+ *
+ * rope pairs adjacent lanes n and n^1: out[n] = t[n]*f1[t,n] + t[n^1]*f2[t,n]
+ * (fast_triton_attn.py:132-141).
+ *
+ * Conventions shared by every entry point:
+ *   - All device pointers are borrowed; the library never allocates device
+ *     memory. Outputs and the workspace are allocated by the caller.
+ *   - Activations and weights are bf16 (the only dtype the reference runs
+ *     with, fast_triton_attn.py:32,103,123). Rotary tables, lse and the
+ *     per-row statistics are fp32.
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*) and is
+ *     asynchronous; nothing synchronises the host.
+ *   - A return of 0 means success. Negative values are argument errors found
+ *     on the host before anything is launched; MEA_ERR_LAUNCH reports a HIP
+ *     launch error. mea_strerror() names every code.
+ *   - Tensors are dense row-major in the shapes documented per argument.
+ *     Pointers must be 16-byte aligned.
+ *
+ * Supported shapes: N in {64, 128}; C a multiple of 256 with C <= 1024 for
+ * the backward pass (C <= 4096 forward); H >= 1; B, T >= 1; T <= T_max.
+ */
+#ifndef MEA_H
+#define MEA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Shape of one block invocation. */
+typedef struct mea_desc {
+  int64_t B;      /* batch */
+  int64_t T;      /* sequence length */
+  int64_t C;      /* model width (x is B x T x C) */
+  int64_t H;      /* heads */
+  int64_t N;      /* head width */
+  int64_t T_max;  /* rows of the rotary tables, >= T */
+  float eps;      /* RMSNorm epsilon; the reference default is 1e-6 (fast_triton_attn.py:681) */
+} mea_desc;
+
+enum {
+  MEA_OK = 0,
+  MEA_ERR_NULL = -1,        /* a required pointer is NULL */
+  MEA_ERR_SHAPE = -2,       /* B, T, H or T_max out of range */
+  MEA_ERR_HEAD_DIM = -3,    /* N not supported */
+  MEA_ERR_MODEL_DIM = -4,   /* C not supported */
+  MEA_ERR_WORKSPACE = -5,   /* workspace smaller than mea_workspace_bytes() */
+  MEA_ERR_ALIGN = -6,       /* a pointer is not 16-byte aligned */
+  MEA_ERR_EPS = -7,         /* eps not finite and positive */
+  MEA_ERR_LAUNCH = -8       /* HIP reported an error at launch */
+};
+
+/* Which pass a workspace size is asked for. */
+enum { MEA_PASS_FWD = 0, MEA_PASS_BWD = 1 };
+
+/*
+ * Workspace bytes needed by mea_fwd (pass 0) or mea_bwd (pass 1).
+ * Returns 0 when the descriptor is invalid.
+ * Replaces the torch.empty transients of FusedAttentionFunction.forward
+ * (fast_triton_attn.py:381,391-394,447) and .backward (:505-506,518-524,560).
+ */
+size_t mea_workspace_bytes(const mea_desc* d, int pass);
+
+/*
+ * Forward of the block. Replaces FusedAttentionFunction.forward
+ * (fast_triton_attn.py:375-479): rms_norm_kernel (:12-34),
+ * fused_qkvg_norm_rope_kernel (:36-144), aten flash attention (:438),
+ * gate_repack_kernel (:146-176) and F.linear (:460).
+ *
+ *   x        (B, T, C) bf16
+ *   wq..wg   (H*N, C)  bf16        nn.Linear.weight of q/k/v/g_proj
+ *   wo       (C, H*N)  bf16        nn.Linear.weight of o_proj
+ *   f1, f2   (T_max, N) fp32       rotary tables (rows 0..T-1 are read)
+ *   y        (B, T, C) bf16        output
+ *   o_save   (B, T, H*N) bf16      attention output, saved for mea_bwd (:465)
+ *   lse_save (B, H, T) fp32        natural-log softmax normaliser (:465)
+ *            o_save and lse_save may be NULL together (inference).
+ */
+int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk,
+            const void* wv, const void* wg, const void* wo, const float* f1,
+            const float* f2, void* y, void* o_save, float* lse_save, void* ws,
+            size_t ws_bytes, void* stream);
+
+/*
+ * Backward of the block. Replaces FusedAttentionFunction.backward
+ * (fast_triton_attn.py:481-675), with the exact q/k RMSNorm and rotary
+ * backward (valid for any rotary table whose 2x2 pair blocks are invertible,
+ * which every RoPE/YaRN table with a positive temperature is).
+ *
+ *   dy                  (B, T, C) bf16     gradient of y
+ *   x, wq..wo, f1, f2   as in mea_fwd
+ *   o_save, lse_save    as written by mea_fwd
+ *   dx                  (B, T, C) bf16     out
+ *   dwq, dwk, dwv, dwg  (H*N, C) bf16      out
+ *   dwo                 (C, H*N) bf16      out
+ *   df1, df2            (T_max, N) fp32    out, rows 0..T-1 written; both may
+ *                                          be NULL to skip the table gradient
+ */
+int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq,
+            const void* wk, const void* wv, const void* wg, const void* wo,
+            const float* f1, const float* f2, const void* o_save,
+            const float* lse_save, void* dx, void* dwq, void* dwk, void* dwv,
+            void* dwg, void* dwo, float* df1, float* df2, void* ws,
+            size_t ws_bytes, void* stream);
+
+/*
+ * Stage: input RMSNorm + q/k/v/g projection + per-head q/k RMSNorm + rotary +
+ * sigmoid. Replaces rms_norm_kernel(_recompute) and
+ * fused_qkvg_norm_rope_kernel(_recompute) (fast_triton_attn.py:12-144,
+ * 181-332).
+ *
+ *   q, k, v  (B, H, T, N) bf16   rotated q/k, plain v
+ *   sig      (B, T, H*N) bf16    sigmoid(a_g)
+ *   rx       (B, T) fp32         1/rms of x rows          (may be NULL)
+ *   rq, rk   (B, H, T) fp32      1/rms of a_q, a_k rows   (may be NULL)
+ */
+int mea_qkvg_proj(const mea_desc* d, const void* x, const void* wq,
+                  const void* wk, const void* wv, const void* wg,
+                  const float* f1, const float* f2, void* q, void* k, void* v,
+                  void* sig, float* rx, float* rq, float* rk, void* stream);
+
+/*
+ * Stage: causal flash attention forward with scale 1/sqrt(N). Replaces
+ * aten._scaled_dot_product_flash_attention (fast_triton_attn.py:425-444).
+ *
+ *   q, k, v  (B, H, T, N) bf16
+ *   o        (B, T, H*N) bf16     out
+ *   lse      (B, H, T) fp32       out (may be NULL)
+ */
+int mea_attn_fwd(const mea_desc* d, const void* q, const void* k,
+                 const void* v, void* o, float* lse, void* stream);
+
+/*
+ * Stage: output gate and projection, y = (o * sig) W_o^T. Replaces
+ * gate_repack_kernel (fast_triton_attn.py:146-176) and F.linear (:460).
+ *
+ *   o, sig   (B, T, H*N) bf16
+ *   wo       (C, H*N) bf16
+ *   y        (B, T, C) bf16       out
+ */
+int mea_gate_oproj(const mea_desc* d, const void* o, const void* sig,
+                   const void* wo, void* y, void* stream);
+
+/* Text for a status code returned by any entry point. */
+const char* mea_strerror(int code);
+
+/*
+ * Kernel timing diagnostics (no counterpart in the reference; used by the
+ * benchmark). While enabled, every kernel the library launches is bracketed
+ * by a pair of HIP events recorded on the stream it is launched on.
+ *   mea_profile_enable(1)  clears previous records and starts recording;
+ *   mea_profile_enable(0)  stops recording (records are kept);
+ *   mea_profile_read(k, &count, &total_ms) waits for the recorded events of
+ *     kernel k and returns its launch count and summed duration;
+ *   mea_profile_kernel_name(k) names kernel k, NULL past the last one.
+ * Recording is process-wide and serialised by a mutex.
+ */
+int mea_profile_enable(int on);
+int mea_profile_read(int kernel, int* count, double* total_ms);
+const char* mea_profile_kernel_name(int kernel);
+
+/* Library version string. */
+const char* mea_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEA_H */

@@ -1,0 +1,438 @@
+// C ABI of the attention block: argument validation, workspace layout and
+// the launch sequence of each pass. Declarations and contracts: include/mea.h.
+#include <math.h>
+#include <stdint.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/mea.h"
+#include "kernels.h"
+
+namespace {
+
+using mea::bf16_bits;
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Number of token slices the weight-gradient reduction is split into.
+inline int dw_splits(int64_t M) {
+  int64_t s = (M + 8191) / 8192;
+  if (s < 1) s = 1;
+  if (s > 16) s = 16;
+  return (int)s;
+}
+
+// Byte offsets of every transient inside the workspace.
+struct Layout {
+  size_t q, k, v, sig, o;                    // forward
+  size_t dO, daq, dak, dav, dag;             // backward
+  size_t rx, rq, rk, delta, woT, wcatT, part;
+  size_t total;
+};
+
+Layout make_layout(const mea_desc& d, int pass) {
+  const size_t M = (size_t)(d.B * d.T), HN = (size_t)(d.H * d.N), C = (size_t)d.C;
+  const size_t act = align_up(M * HN * 2), stat = align_up(M * (size_t)d.H * 4);
+  Layout L = {};
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes); return o; };
+  L.q = take(act);
+  L.k = take(act);
+  L.v = take(act);
+  L.sig = take(act);
+  if (pass == MEA_PASS_FWD) {
+    L.o = take(act);
+  } else {
+    L.dO = take(act);
+    L.daq = take(act);
+    L.dak = take(act);
+    L.dav = take(act);
+    L.dag = take(act);
+    L.rx = take(M * 4);
+    L.rq = take(stat);
+    L.rk = take(stat);
+    L.delta = take(stat);
+    L.woT = take(HN * C * 2);
+    L.wcatT = take(C * 4 * HN * 2);
+    L.part = take((size_t)dw_splits((int64_t)M) * (4 * HN * C + C * HN) * 4);
+  }
+  L.total = off;
+  return L;
+}
+
+int validate(const mea_desc* d, int pass) {
+  if (d == nullptr) return MEA_ERR_NULL;
+  if (d->B < 1 || d->T < 1 || d->H < 1 || d->T_max < d->T) return MEA_ERR_SHAPE;
+  if (d->N != 64 && d->N != 128) return MEA_ERR_HEAD_DIM;
+  if (d->C < 256 || d->C % 256 != 0) return MEA_ERR_MODEL_DIM;
+  if (pass == MEA_PASS_BWD && d->C > 1024) return MEA_ERR_MODEL_DIM;
+  if (pass == MEA_PASS_FWD && d->C > 4096) return MEA_ERR_MODEL_DIM;
+  if (!(d->eps > 0.f) || !isfinite(d->eps)) return MEA_ERR_EPS;
+  // All row and element indices used by the kernels fit in 31 bits.
+  const int64_t M = d->B * d->T, HN = d->H * d->N;
+  if (M >= (INT64_C(1) << 31) || HN >= 65536 || d->B * d->H * d->T >= (INT64_C(1) << 31) ||
+      d->T_max * d->N >= (INT64_C(1) << 31))
+    return MEA_ERR_SHAPE;
+  return MEA_OK;
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_ptrs(std::initializer_list<const void*> ps) {
+  for (const void* p : ps) {
+    if (p == nullptr) return MEA_ERR_NULL;
+    if (!aligned16(p)) return MEA_ERR_ALIGN;
+  }
+  return MEA_OK;
+}
+
+#define MEA_TRY(expr)                                  \
+  do {                                                 \
+    if ((expr) != hipSuccess) return MEA_ERR_LAUNCH;   \
+  } while (0)
+
+template <class T>
+T* at(void* ws, size_t off) {
+  return reinterpret_cast<T*>(static_cast<unsigned char*>(ws) + off);
+}
+
+// ---- kernel timing diagnostics -------------------------------------------
+enum KernelId {
+  K_QKVG_PROJ, K_ATTN_FWD, K_GATE_OPROJ, K_TRANSPOSE, K_ZERO, K_DZ_GATE_BWD,
+  K_ATTN_BWD_DQ, K_ATTN_BWD_DKDV, K_DW_PARTIAL, K_DW_REDUCE, K_DX, K_COUNT
+};
+const char* const kKernelNames[K_COUNT] = {
+    "qkvg_proj", "attn_fwd", "gate_oproj", "transpose", "zero_f32", "dz_gate_bwd",
+    "attn_bwd_dq", "attn_bwd_dkdv", "dw_partial", "dw_reduce", "dx"};
+
+struct ProfRec {
+  int kernel;
+  hipEvent_t a, b;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRec> g_prof;
+std::vector<hipEvent_t> g_pool;
+
+hipEvent_t pool_event() {
+  if (!g_pool.empty()) {
+    hipEvent_t e = g_pool.back();
+    g_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Runs `launch` (which returns a hipError_t); when profiling is on, brackets
+// it with events on stream s.
+template <class F>
+hipError_t timed(int kernel, hipStream_t s, F launch) {
+  std::unique_lock<std::mutex> lk(g_prof_mu);
+  if (!g_prof_on) {
+    lk.unlock();
+    return launch();
+  }
+  hipEvent_t a = pool_event(), b = pool_event();
+  if (a == nullptr || b == nullptr) return hipErrorOutOfMemory;
+  (void)hipEventRecord(a, s);
+  const hipError_t e = launch();
+  (void)hipEventRecord(b, s);
+  g_prof.push_back({kernel, a, b});
+  return e;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mea_workspace_bytes(const mea_desc* d, int pass) {
+  if (pass != MEA_PASS_FWD && pass != MEA_PASS_BWD) return 0;
+  if (validate(d, pass) != MEA_OK) return 0;
+  return make_layout(*d, pass).total;
+}
+
+int mea_qkvg_proj(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv,
+                  const void* wg, const float* f1, const float* f2, void* q, void* k, void* v, void* sig,
+                  float* rx, float* rq, float* rk, void* stream) {
+  int rc = validate(d, MEA_PASS_FWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({x, wq, wk, wv, wg, f1, f2, q, k, v, sig});
+  if (rc != MEA_OK) return rc;
+  mea::ProjParams p;
+  p.x = static_cast<const bf16_bits*>(x);
+  p.wq = static_cast<const bf16_bits*>(wq);
+  p.wk = static_cast<const bf16_bits*>(wk);
+  p.wv = static_cast<const bf16_bits*>(wv);
+  p.wg = static_cast<const bf16_bits*>(wg);
+  p.f1 = f1;
+  p.f2 = f2;
+  p.q = static_cast<bf16_bits*>(q);
+  p.k = static_cast<bf16_bits*>(k);
+  p.v = static_cast<bf16_bits*>(v);
+  p.sig = static_cast<bf16_bits*>(sig);
+  p.rx = rx;
+  p.rq = rq;
+  p.rk = rk;
+  p.M = (int)(d->B * d->T);
+  p.T = (int)d->T;
+  p.C = (int)d->C;
+  p.H = (int)d->H;
+  p.eps = d->eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MEA_TRY(timed(K_QKVG_PROJ, s, [&] { return mea::launch_qkvg_proj(p, (int)d->N, s); }));
+  return MEA_OK;
+}
+
+int mea_attn_fwd(const mea_desc* d, const void* q, const void* k, const void* v, void* o, float* lse,
+                 void* stream) {
+  int rc = validate(d, MEA_PASS_FWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({q, k, v, o});
+  if (rc != MEA_OK) return rc;
+  mea::AttnFwdParams p;
+  p.q = static_cast<const bf16_bits*>(q);
+  p.k = static_cast<const bf16_bits*>(k);
+  p.v = static_cast<const bf16_bits*>(v);
+  p.o = static_cast<bf16_bits*>(o);
+  p.lse = lse;
+  p.B = (int)d->B;
+  p.H = (int)d->H;
+  p.T = (int)d->T;
+  p.sl2e = (float)(1.0 / sqrt((double)d->N) * 1.4426950408889634);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MEA_TRY(timed(K_ATTN_FWD, s, [&] { return mea::launch_attn_fwd(p, (int)d->N, s); }));
+  return MEA_OK;
+}
+
+int mea_gate_oproj(const mea_desc* d, const void* o, const void* sig, const void* wo, void* y, void* stream) {
+  int rc = validate(d, MEA_PASS_FWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({o, sig, wo, y});
+  if (rc != MEA_OK) return rc;
+  mea::OprojParams p;
+  p.o = static_cast<const bf16_bits*>(o);
+  p.sig = static_cast<const bf16_bits*>(sig);
+  p.wo = static_cast<const bf16_bits*>(wo);
+  p.y = static_cast<bf16_bits*>(y);
+  p.M = (int)(d->B * d->T);
+  p.C = (int)d->C;
+  p.HN = (int)(d->H * d->N);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MEA_TRY(timed(K_GATE_OPROJ, s, [&] { return mea::launch_gate_oproj(p, s); }));
+  return MEA_OK;
+}
+
+int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+            const void* wo, const float* f1, const float* f2, void* y, void* o_save, float* lse_save, void* ws,
+            size_t ws_bytes, void* stream) {
+  int rc = validate(d, MEA_PASS_FWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({x, wq, wk, wv, wg, wo, f1, f2, y, ws});
+  if (rc != MEA_OK) return rc;
+  if ((o_save == nullptr) != (lse_save == nullptr)) return MEA_ERR_NULL;
+  if (o_save != nullptr && !aligned16(o_save)) return MEA_ERR_ALIGN;
+  const Layout L = make_layout(*d, MEA_PASS_FWD);
+  if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
+  void* q = at<void>(ws, L.q);
+  void* k = at<void>(ws, L.k);
+  void* v = at<void>(ws, L.v);
+  void* sig = at<void>(ws, L.sig);
+  void* o = o_save != nullptr ? o_save : at<void>(ws, L.o);
+  rc = mea_qkvg_proj(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, nullptr, nullptr, nullptr, stream);
+  if (rc != MEA_OK) return rc;
+  rc = mea_attn_fwd(d, q, k, v, o, lse_save, stream);
+  if (rc != MEA_OK) return rc;
+  return mea_gate_oproj(d, o, sig, wo, y, stream);
+}
+
+int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, const void* wk, const void* wv,
+            const void* wg, const void* wo, const float* f1, const float* f2, const void* o_save,
+            const float* lse_save, void* dx, void* dwq, void* dwk, void* dwv, void* dwg, void* dwo, float* df1,
+            float* df2, void* ws, size_t ws_bytes, void* stream) {
+  int rc = validate(d, MEA_PASS_BWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, dx, dwq, dwk, dwv, dwg, dwo, ws});
+  if (rc != MEA_OK) return rc;
+  if ((df1 == nullptr) != (df2 == nullptr)) return MEA_ERR_NULL;
+  if (df1 != nullptr && (!aligned16(df1) || !aligned16(df2))) return MEA_ERR_ALIGN;
+  const Layout L = make_layout(*d, MEA_PASS_BWD);
+  if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = (int)(d->B * d->T), T = (int)d->T, H = (int)d->H, N = (int)d->N, C = (int)d->C;
+  const int HN = H * N;
+
+  bf16_bits* q = at<bf16_bits>(ws, L.q);
+  bf16_bits* k = at<bf16_bits>(ws, L.k);
+  bf16_bits* v = at<bf16_bits>(ws, L.v);
+  bf16_bits* sig = at<bf16_bits>(ws, L.sig);
+  bf16_bits* dO = at<bf16_bits>(ws, L.dO);
+  bf16_bits* daq = at<bf16_bits>(ws, L.daq);
+  bf16_bits* dak = at<bf16_bits>(ws, L.dak);
+  bf16_bits* dav = at<bf16_bits>(ws, L.dav);
+  bf16_bits* dag = at<bf16_bits>(ws, L.dag);
+  float* rx = at<float>(ws, L.rx);
+  float* rq = at<float>(ws, L.rq);
+  float* rk = at<float>(ws, L.rk);
+  float* delta = at<float>(ws, L.delta);
+  bf16_bits* woT = at<bf16_bits>(ws, L.woT);
+  bf16_bits* wcatT = at<bf16_bits>(ws, L.wcatT);
+  float* part = at<float>(ws, L.part);
+
+  // Weight transposes (k-contiguous B operands for dZ and dx).
+  MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_transpose(static_cast<const bf16_bits*>(wo), C, HN, HN, woT, C, 0, s); }));
+  const void* wp[4] = {wq, wk, wv, wg};
+  for (int j = 0; j < 4; ++j)
+    MEA_TRY(timed(K_TRANSPOSE, s, [&] {
+      return mea::launch_transpose(static_cast<const bf16_bits*>(wp[j]), HN, C, C, wcatT, 4 * HN, j * HN, s);
+    }));
+  if (df1 != nullptr) {
+    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df1, (size_t)T * N, s); }));
+    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df2, (size_t)T * N, s); }));
+  }
+
+  // Recompute q, k, v, sigmoid(g) and the three RMS statistics.
+  rc = mea_qkvg_proj(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, stream);
+  if (rc != MEA_OK) return rc;
+
+  mea::DzParams dz;
+  dz.dy = static_cast<const bf16_bits*>(dy);
+  dz.woT = woT;
+  dz.o = static_cast<const bf16_bits*>(o_save);
+  dz.sig = sig;
+  dz.rx = rx;
+  dz.dO = dO;
+  dz.dag = dag;
+  dz.delta = delta;
+  dz.M = M;
+  dz.T = T;
+  dz.C = C;
+  dz.H = H;
+  dz.N = N;
+  MEA_TRY(timed(K_DZ_GATE_BWD, s, [&] { return mea::launch_dz_gate_bwd(dz, s); }));
+
+  mea::AttnBwdParams ab;
+  ab.q = q;
+  ab.k = k;
+  ab.v = v;
+  ab.dO = dO;
+  ab.lse = lse_save;
+  ab.delta = delta;
+  ab.f1 = f1;
+  ab.f2 = f2;
+  ab.rx = rx;
+  ab.rq = rq;
+  ab.rk = rk;
+  ab.daq = daq;
+  ab.dak = dak;
+  ab.dav = dav;
+  ab.df1 = df1;
+  ab.df2 = df2;
+  ab.B = (int)d->B;
+  ab.H = H;
+  ab.T = T;
+  ab.scale = (float)(1.0 / sqrt((double)N));
+  ab.sl2e = (float)(1.0 / sqrt((double)N) * 1.4426950408889634);
+  MEA_TRY(timed(K_ATTN_BWD_DQ, s, [&] { return mea::launch_attn_bwd_dq(ab, N, s); }));
+  MEA_TRY(timed(K_ATTN_BWD_DKDV, s, [&] { return mea::launch_attn_bwd_dkdv(ab, N, s); }));
+
+  mea::DwParams dw;
+  dw.daq = daq;
+  dw.dak = dak;
+  dw.dav = dav;
+  dw.dag = dag;
+  dw.x = static_cast<const bf16_bits*>(x);
+  dw.dy = static_cast<const bf16_bits*>(dy);
+  dw.o = static_cast<const bf16_bits*>(o_save);
+  dw.sig = sig;
+  dw.part = part;
+  dw.M = M;
+  dw.C = C;
+  dw.HN = HN;
+  dw.splits = dw_splits(M);
+  MEA_TRY(timed(K_DW_PARTIAL, s, [&] { return mea::launch_dw_partial(dw, s); }));
+  mea::DwReduceParams dr;
+  dr.part = part;
+  dr.dwq = static_cast<bf16_bits*>(dwq);
+  dr.dwk = static_cast<bf16_bits*>(dwk);
+  dr.dwv = static_cast<bf16_bits*>(dwv);
+  dr.dwg = static_cast<bf16_bits*>(dwg);
+  dr.dwo = static_cast<bf16_bits*>(dwo);
+  dr.C = C;
+  dr.HN = HN;
+  dr.splits = dw.splits;
+  MEA_TRY(timed(K_DW_REDUCE, s, [&] { return mea::launch_dw_reduce(dr, s); }));
+
+  mea::DxParams dxp;
+  dxp.daq = daq;
+  dxp.dak = dak;
+  dxp.dav = dav;
+  dxp.dag = dag;
+  dxp.wcatT = wcatT;
+  dxp.x = static_cast<const bf16_bits*>(x);
+  dxp.rx = rx;
+  dxp.dx = static_cast<bf16_bits*>(dx);
+  dxp.M = M;
+  dxp.C = C;
+  dxp.HN = HN;
+  MEA_TRY(timed(K_DX, s, [&] { return mea::launch_dx(dxp, s); }));
+  return MEA_OK;
+}
+
+const char* mea_strerror(int code) {
+  switch (code) {
+    case MEA_OK: return "ok";
+    case MEA_ERR_NULL: return "a required pointer is NULL (or only one of a pair was given)";
+    case MEA_ERR_SHAPE: return "B, T, H must be >= 1, T <= T_max, and indices must fit 31 bits";
+    case MEA_ERR_HEAD_DIM: return "head width N must be 64 or 128";
+    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 256 (<= 1024 backward, <= 4096 forward)";
+    case MEA_ERR_WORKSPACE: return "workspace smaller than mea_workspace_bytes()";
+    case MEA_ERR_ALIGN: return "a pointer is not 16-byte aligned";
+    case MEA_ERR_EPS: return "eps must be finite and positive";
+    case MEA_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+const char* mea_version(void) { return "mea 0.1.0 gfx950"; }
+
+int mea_profile_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (on && !g_prof_on) {
+    for (const ProfRec& r : g_prof) {
+      (void)hipEventSynchronize(r.b);
+      g_pool.push_back(r.a);
+      g_pool.push_back(r.b);
+    }
+    g_prof.clear();
+  }
+  g_prof_on = on != 0;
+  return MEA_OK;
+}
+
+int mea_profile_read(int kernel, int* count, double* total_ms) {
+  if (kernel < 0 || kernel >= K_COUNT || count == nullptr || total_ms == nullptr) return MEA_ERR_NULL;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  int n = 0;
+  double ms = 0.0;
+  for (const ProfRec& r : g_prof) {
+    if (r.kernel != kernel) continue;
+    if (hipEventSynchronize(r.b) != hipSuccess) return MEA_ERR_LAUNCH;
+    float t = 0.f;
+    if (hipEventElapsedTime(&t, r.a, r.b) != hipSuccess) return MEA_ERR_LAUNCH;
+    ms += t;
+    ++n;
+  }
+  *count = n;
+  *total_ms = ms;
+  return MEA_OK;
+}
+
+const char* mea_profile_kernel_name(int kernel) {
+  return kernel >= 0 && kernel < K_COUNT ? kKernelNames[kernel] : nullptr;
+}
+
+}  // extern "C"

@@ -1,0 +1,116 @@
+// Device helpers shared by the gfx950 kernels of the attention block.
+//
+// MFMA convention used throughout (v_mfma_f32_16x16x32_bf16, one wave of 64
+// lanes, lane = 16*g + c with g in 0..3 and c in 0..15):
+//   A operand (16 rows x 32 k):  lane holds row c, k = 8g .. 8g+7
+//   B operand (32 k x 16 cols):  lane holds col c, k = 8g .. 8g+7
+//   D (16 x 16 fp32):            lane holds col c, rows 4g .. 4g+3
+// Only the D layout matters for correctness of a plain product: the k order
+// inside A and B is the same function of (g, element), so any consistent
+// permutation of k between the two operands gives the same sum. The attention
+// kernels rely on that to feed an accumulator straight back as an operand.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mea {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t bf16_bits;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x4 mfma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// bf16 bit patterns <-> fp32.
+__device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf2f(bf16_bits h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (hardware conversion on gfx950).
+__device__ __forceinline__ bf16_bits f2bf(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(bf16_bits, b);
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = lo_bf(v[i]);
+    f[2 * i + 1] = hi_bf(v[i]);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack2(f[2 * i], f[2 * i + 1]);
+  return v;
+}
+
+__device__ __forceinline__ bf16x8 as_frag(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x8 frag_from2(const u32x2& a, const u32x2& b) {
+  u32x4 v = {a[0], a[1], b[0], b[1]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// 16-byte global load / store.
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Cross-lane helpers. xor 1 / xor 2 use DPP quad permutes; wider distances go
+// through ds_bpermute (no memory traffic).
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+__device__ __forceinline__ float xor1(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float xor2(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+}
+// Sum over the 16 lanes that share g (lane = 16g + c).
+__device__ __forceinline__ float sum16(float v) {
+  v += xor1(v);
+  v += xor2(v);
+  v += shfl_xor(v, 4);
+  v += shfl_xor(v, 8);
+  return v;
+}
+// Sum / max over the 4 lane groups g that share c.
+__device__ __forceinline__ float sum_g(float v) {
+  v += shfl_xor(v, 16);
+  v += shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float max_g(float v) {
+  v = fmaxf(v, shfl_xor(v, 16));
+  v = fmaxf(v, shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float sigmoidf(float a) { return 1.0f / (1.0f + __expf(-a)); }
+
+// Block-id remapping so that consecutive logical tiles run on the same XCD.
+// The hardware hands workgroup L to XCD L % 8; logical tile ids
+// [start(x), start(x)+count(x)) are made to run on XCD x, which keeps
+// neighbouring tiles (that share operand rows) inside one L2.
+__device__ __forceinline__ int xcd_remap(int L, int G) {
+  const int x = L & 7, i = L >> 3;
+  const int q = G >> 3, r = G & 7;
+  const int start = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+  return start + i;
+}
+
+}  // namespace mea

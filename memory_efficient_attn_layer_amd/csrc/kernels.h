@@ -1,0 +1,118 @@
+// Parameter blocks and host-side launchers of the block's kernels.
+// Every launcher enqueues on `stream` and returns hipGetLastError().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mea {
+
+typedef uint16_t bf16_bits;
+
+// Input RMSNorm + q/k/v/g projection + q/k head RMSNorm + rotary + sigmoid.
+struct ProjParams {
+  const bf16_bits* x;                       // (M, C)
+  const bf16_bits *wq, *wk, *wv, *wg;       // (H*N, C)
+  const float *f1, *f2;                     // (T_max, N)
+  bf16_bits *q, *k, *v;                     // (B, H, T, N)
+  bf16_bits* sig;                           // (M, H*N)
+  float* rx;                                // (M) or null
+  float *rq, *rk;                           // (B, H, T) or null
+  int M, T, C, H;
+  float eps;
+};
+hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s);
+
+// Causal flash attention forward.
+struct AttnFwdParams {
+  const bf16_bits *q, *k, *v;               // (B, H, T, N)
+  bf16_bits* o;                             // (B, T, H*N)
+  float* lse;                               // (B, H, T) or null
+  int B, H, T;
+  float sl2e;                               // softmax scale * log2(e)
+};
+hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s);
+
+// Causal flash attention backward fused with the q/k RMSNorm + rotary
+// backward and the input-RMSNorm row scale of the projection gradients.
+struct AttnBwdParams {
+  const bf16_bits *q, *k, *v, *dO;          // (B, H, T, N)
+  const float *lse, *delta;                 // (B, H, T)
+  const float *f1, *f2;                     // (T_max, N)
+  const float* rx;                          // (M)
+  const float *rq, *rk;                     // (B, H, T)
+  bf16_bits *daq, *dak, *dav;               // (M, H*N), rows scaled by rx
+  float *df1, *df2;                         // (T, N) accumulators or null
+  int B, H, T;
+  float scale, sl2e;
+};
+hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s);
+hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s);
+
+// y = (o * sig) Wo^T.
+struct OprojParams {
+  const bf16_bits *o, *sig;                 // (M, HN)
+  const bf16_bits* wo;                      // (C, HN)
+  bf16_bits* y;                             // (M, C)
+  int M, C, HN;
+};
+hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s);
+
+// dZ = dy Wo, then the gate backward:
+//   dO = dZ * sig            -> (B, H, T, N)
+//   da_g = rx * dZ * O * sig * (1 - sig)   -> (M, HN)
+//   delta = rowsum_N(dO * O) -> (B, H, T)
+struct DzParams {
+  const bf16_bits* dy;                      // (M, C)
+  const bf16_bits* woT;                     // (HN, C)
+  const bf16_bits *o, *sig;                 // (M, HN)
+  const float* rx;                          // (M)
+  bf16_bits* dO;                            // (B, H, T, N)
+  bf16_bits* dag;                           // (M, HN)
+  float* delta;                             // (B, H, T)
+  int M, T, C, H, N;
+};
+hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s);
+
+// acc = [daq|dak|dav|dag] Wcat  (rows pre-scaled by rx), then the input
+// RMSNorm backward: dx = acc - x * rx^2 * (acc . x) / C.
+struct DxParams {
+  const bf16_bits *daq, *dak, *dav, *dag;   // (M, HN)
+  const bf16_bits* wcatT;                   // (C, 4*HN)
+  const bf16_bits* x;                       // (M, C)
+  const float* rx;                          // (M)
+  bf16_bits* dx;                            // (M, C)
+  int M, C, HN;
+};
+hipError_t launch_dx(const DxParams& p, hipStream_t s);
+
+// Weight gradients, split over tokens into fp32 partial sums:
+//   dWcat = [daq|dak|dav|dag]^T x        (4*HN, C)
+//   dWo   = dy^T (o * sig)               (C, HN)
+struct DwParams {
+  const bf16_bits *daq, *dak, *dav, *dag;   // (M, HN)
+  const bf16_bits* x;                       // (M, C)
+  const bf16_bits* dy;                      // (M, C)
+  const bf16_bits *o, *sig;                 // (M, HN)
+  float* part;                              // (splits, 4*HN*C + C*HN)
+  int M, C, HN, splits;
+};
+hipError_t launch_dw_partial(const DwParams& p, hipStream_t s);
+// Sums the partials and writes the five bf16 weight gradients.
+struct DwReduceParams {
+  const float* part;
+  bf16_bits *dwq, *dwk, *dwv, *dwg, *dwo;
+  int C, HN, splits;
+};
+hipError_t launch_dw_reduce(const DwReduceParams& p, hipStream_t s);
+
+// out(cols, rows) = in(rows, cols)^T for a bf16 matrix with leading
+// dimension ld_in; writes into out with leading dimension ld_out starting at
+// column col_off.
+hipError_t launch_transpose(const bf16_bits* in, int rows, int cols, int ld_in, bf16_bits* out,
+                            int ld_out, int col_off, hipStream_t s);
+
+// Fills n floats with zero (a kernel, so it is safe inside captured graphs).
+hipError_t launch_zero_f32(float* p, size_t n, hipStream_t s);
+
+}  // namespace mea

@@ -1,0 +1,70 @@
+"""Shared helpers of the GPU parity tests (not collected by pytest).
+
+Tolerances (the block's stated contract, against the fp32 eager oracle on
+identical bf16-rounded inputs):
+  * bf16 outputs (y and stage outputs): max |gpu - ref| <= 2e-2 * max |ref|
+    and relative Frobenius error <= 2e-2;
+  * gradients (dx, all five weight gradients, both table gradients):
+    relative Frobenius error ||gpu - ref|| / ||ref|| <= 3e-2.
+"""
+from __future__ import annotations
+
+import torch
+
+from memory_efficient_attn_layer_amd.attention import FusedAttentionFunction
+from memory_efficient_attn_layer_amd.synthetic import Workload, make_inputs
+from oracle import block as ob
+
+OUT_TOL = 2e-2
+GRAD_TOL = 3e-2
+
+
+def rel_fro(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def max_rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def assert_out_close(name: str, got: torch.Tensor, ref: torch.Tensor, tol: float = OUT_TOL):
+    assert torch.isfinite(got.float()).all(), f"{name}: non-finite values"
+    mr, rf = max_rel(got, ref), rel_fro(got, ref)
+    assert mr <= tol and rf <= tol, f"{name}: max-abs/max|ref| = {mr:.3e}, rel-fro = {rf:.3e} (tol {tol})"
+
+
+def assert_grad_close(name: str, got: torch.Tensor, ref: torch.Tensor, tol: float = GRAD_TOL):
+    assert torch.isfinite(got.float()).all(), f"{name}: non-finite values"
+    rf = rel_fro(got, ref)
+    assert rf <= tol, f"{name}: rel-fro = {rf:.3e} (tol {tol})"
+
+
+def gpu_block(inp: dict, H: int, N: int, table_grad: bool = True, eps: float = 1e-6):
+    """fused_attn forward + backward on the GPU with loss = sum(y * dy)."""
+    names = ("x", "wq", "wk", "wv", "wg", "wo", "f1", "f2")
+    leaf = {n: inp[n].detach().cuda().clone().requires_grad_(table_grad or n not in ("f1", "f2")) for n in names}
+    y = FusedAttentionFunction.apply(*(leaf[n] for n in names), H, N, eps)
+    y.backward(inp["dy"].cuda())
+    torch.cuda.synchronize()
+    out = {"y": y.detach()}
+    for n in names:
+        out["d" + n] = None if leaf[n].grad is None else leaf[n].grad.detach()
+    return out
+
+
+def check_block(w: Workload, B: int | None = None, seed: int | None = None, table_grad: bool = True, **over):
+    """Full block parity on workload ``w`` (optionally a batch slice)."""
+    inp = make_inputs(w, dtype=torch.bfloat16, B=B, seed=seed)
+    inp.update(over)
+    got = gpu_block(inp, w.H, w.N, table_grad=table_grad)
+    ref = ob.block_grads(inp, w.H, w.N, dtype=torch.float32)
+    assert_out_close("y", got["y"], ref["y"])
+    for k in ("dx", "dwq", "dwk", "dwv", "dwg", "dwo"):
+        assert_grad_close(k, got[k], ref[k])
+    if table_grad:
+        T = inp["x"].shape[1]
+        assert_grad_close("df1", got["df1"][:T], ref["df1"][:T])
+        assert_grad_close("df2", got["df2"][:T], ref["df2"][:T])
+    return got, ref

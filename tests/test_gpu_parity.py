@@ -1,0 +1,149 @@
+"""GPU parity of the HIP block against the CPU fp32 oracle (and its stages).
+
+Every case prints its shape through the test id. Sizes are chosen so the CPU
+oracle finishes in seconds; full-size properties are covered in
+test_gpu_fullsize.py.
+"""
+import math
+
+import pytest
+import torch
+
+from memory_efficient_attn_layer_amd import stages
+from memory_efficient_attn_layer_amd.synthetic import WORKLOADS, Workload, make_inputs
+from oracle import block as ob
+from tests.parity_util import assert_grad_close, assert_out_close, check_block, gpu_block
+
+pytestmark = pytest.mark.gpu
+
+W0, W1, W2, W3 = (WORKLOADS[i] for i in range(4))
+
+
+def _w(name, B, T, C, H, N, scale=1.0, L0=None):
+    return Workload(99, name, B, T, C, H, N, scale, L0)
+
+
+STAGE_CASES = [
+    ("cfg0", W0, None),
+    ("cfg1-b1-t1024", _w("c1", 1, 1024, 512, 8, 64), None),
+    ("cfg3-b1-t512", _w("c3", 1, 512, 1024, 8, 128), None),
+    ("ragged-b3-t77", _w("r", 3, 77, 256, 2, 64), None),
+    ("yarn4-b1-t300", _w("y", 1, 300, 512, 4, 64, 4.0, 128), None),
+]
+
+
+@pytest.mark.parametrize("label,w,B", STAGE_CASES, ids=[c[0] for c in STAGE_CASES])
+def test_stage_qkvg_projection(label, w, B):
+    inp = make_inputs(w, B=B)
+    g = {k: v.cuda() for k, v in inp.items()}
+    q, k, v, sig, rx, rq, rk = stages.qkvg_proj(g["x"], g["wq"], g["wk"], g["wv"], g["wg"], g["f1"], g["f2"],
+                                                w.H, w.N, stats=True)
+    torch.cuda.synchronize()
+    it = ob.block_intermediates(*(inp[n].float() for n in ("x", "wq", "wk", "wv", "wg", "wo", "f1", "f2")),
+                                w.H, w.N)
+    assert_out_close("q", q.transpose(1, 2), it["q"])
+    assert_out_close("k", k.transpose(1, 2), it["k"])
+    assert_out_close("v", v.transpose(1, 2), it["v"])
+    assert_out_close("sig", sig, it["sig"])
+    xf = inp["x"].float()
+    rx_ref = torch.rsqrt(xf.pow(2).mean(-1) + 1e-6)
+    assert_out_close("rx", rx, rx_ref, 1e-4)
+    aq = it["a_q"]
+    rq_ref = torch.rsqrt(aq.pow(2).mean(-1) + 1e-6).transpose(1, 2)
+    assert_out_close("rq", rq, rq_ref, 2e-3)
+
+
+@pytest.mark.parametrize("label,w,B", STAGE_CASES, ids=[c[0] for c in STAGE_CASES])
+def test_stage_attention_forward(label, w, B):
+    Bv = w.B if B is None else B
+    gen = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(Bv, w.H, w.T, w.N, generator=gen).to(torch.bfloat16) for _ in range(3))
+    o, lse = stages.attn_fwd(q.cuda(), k.cuda(), v.cuda(), C=w.C)
+    torch.cuda.synchronize()
+    qf, kf, vf = (t.float().transpose(1, 2) for t in (q, k, v))
+    ref = ob.causal_attention(qf, kf, vf).reshape(Bv, w.T, w.H * w.N)
+    assert_out_close("o", o, ref)
+    s = torch.einsum("bhtn,bhun->bhtu", q.float(), k.float()) / math.sqrt(w.N)
+    s = s.masked_fill(~torch.ones(w.T, w.T, dtype=torch.bool).tril(), float("-inf"))
+    lse_ref = torch.logsumexp(s, -1)
+    assert float((lse.cpu() - lse_ref).abs().max()) < 1e-3
+
+
+@pytest.mark.parametrize("label,w,B", STAGE_CASES, ids=[c[0] for c in STAGE_CASES])
+def test_stage_gate_oproj(label, w, B):
+    Bv = w.B if B is None else B
+    gen = torch.Generator().manual_seed(11)
+    HN = w.H * w.N
+    o = torch.randn(Bv, w.T, HN, generator=gen).to(torch.bfloat16)
+    sig = torch.rand(Bv, w.T, HN, generator=gen).to(torch.bfloat16)
+    wo = ((torch.rand(w.C, HN, generator=gen) * 2 - 1) * 0.5 / math.sqrt(w.C)).to(torch.bfloat16)
+    y = stages.gate_oproj(o.cuda(), sig.cuda(), wo.cuda(), w.H, w.N)
+    torch.cuda.synchronize()
+    ref = (o.float() * sig.float()) @ wo.float().T
+    assert_out_close("y", y, ref)
+
+
+BLOCK_CASES = [
+    ("cfg0-full", W0, None),
+    ("cfg1-b1-t4096", W1, 1),
+    ("cfg2-yarn4-b1-t2048", _w("c2", 1, 2048, 512, 8, 64, 4.0, 8192), None),
+    ("cfg3-b1-t1024", _w("c3", 1, 1024, 1024, 8, 128), None),
+    ("ragged-b3-t77", _w("r", 3, 77, 256, 2, 64), None),
+    ("ragged-b2-t200-n128", _w("r2", 2, 200, 256, 2, 128), None),
+    ("t1-b2", _w("t1", 2, 1, 256, 4, 64), None),
+    ("t129-b1", _w("t129", 1, 129, 512, 8, 64), None),
+    ("c-ne-hn-b2-t160", _w("chn", 2, 160, 512, 4, 64), None),
+    ("yarn8-b2-t300-n128", _w("y8", 2, 300, 256, 2, 128, 8.0, 64), None),
+]
+
+
+@pytest.mark.parametrize("label,w,B", BLOCK_CASES, ids=[c[0] for c in BLOCK_CASES])
+def test_block_forward_backward(label, w, B):
+    check_block(w, B=B)
+
+
+def test_block_without_table_grad_matches():
+    got, _ = check_block(W0, table_grad=False)
+    assert got["df1"] is None and got["df2"] is None
+
+
+def test_zero_o_proj_known_answer():
+    """README.md:35 initialises o_proj to zero: y must be exactly 0 and every
+    gradient except dWo exactly 0."""
+    inp = make_inputs(W0)
+    inp["wo"] = torch.zeros_like(inp["wo"])
+    got = gpu_block(inp, W0.H, W0.N)
+    assert torch.count_nonzero(got["y"]) == 0
+    for k in ("dx", "dwq", "dwk", "dwv", "dwg", "df1", "df2"):
+        assert torch.count_nonzero(got[k]) == 0, k
+    ref = ob.block_grads(inp, W0.H, W0.N)
+    assert_grad_close("dwo", got["dwo"], ref["dwo"])
+
+
+def test_zero_gate_known_answer():
+    """Wg = 0 gives sigmoid = 1/2 exactly: y equals half the projection of o."""
+    inp = make_inputs(W0)
+    inp["wg"] = torch.zeros_like(inp["wg"])
+    g = {k: v.cuda() for k, v in inp.items()}
+    q, k, v, sig = stages.qkvg_proj(g["x"], g["wq"], g["wk"], g["wv"], g["wg"], g["f1"], g["f2"], W0.H, W0.N)
+    assert torch.all(sig == 0.5)
+
+
+def test_deterministic():
+    inp = make_inputs(W0)
+    a = gpu_block(inp, W0.H, W0.N, table_grad=False)
+    b = gpu_block(inp, W0.H, W0.N, table_grad=False)
+    for k in ("y", "dx", "dwq", "dwk", "dwv", "dwg", "dwo"):
+        assert torch.equal(a[k], b[k]), k
+
+
+def test_inference_forward_matches_training_forward():
+    inp = make_inputs(W0)
+    g = {k: v.cuda() for k, v in inp.items()}
+    args = [g[n] for n in ("x", "wq", "wk", "wv", "wg", "wo", "f1", "f2")]
+    from memory_efficient_attn_layer_amd.attention import FusedAttentionFunction
+
+    with torch.no_grad():
+        y0 = FusedAttentionFunction.apply(*args, W0.H, W0.N, 1e-6)
+    y1 = gpu_block(inp, W0.H, W0.N)["y"]
+    assert torch.equal(y0, y1)

@@ -1,0 +1,153 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports
+every function include/mea.h declares, its argument validation returns the
+documented status before touching any pointer, and the Python wrapper
+rejects unsupported inputs before any launch."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from memory_efficient_attn_layer_amd import _lib
+from memory_efficient_attn_layer_amd.attention import FusedAttentionFunction, fused_attn
+from memory_efficient_attn_layer_amd.module import CausalSoftmaxAttention
+from memory_efficient_attn_layer_amd.yarn import Yarn
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mea.h"
+
+
+def _header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mea_\w+)\s*\(", text, flags=re.M)))
+
+
+def _header_enum(name):
+    m = re.search(rf"{name}\s*=\s*(-?\d+)", HEADER.read_text())
+    return int(m.group(1))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} not built; run python -m memory_efficient_attn_layer_amd.build")
+    return _lib.load()
+
+
+def test_library_exports_every_declared_function(lib):
+    declared = _header_functions()
+    assert set(declared) == set(_lib.EXPORTS), (declared, sorted(_lib.EXPORTS))
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_strerror_and_version(lib):
+    for code in range(0, -9, -1):
+        msg = _lib.strerror(code)
+        assert msg and msg != "unknown status", code
+    assert _lib.strerror(-1234) == "unknown status"
+    assert lib.mea_version().decode().startswith("mea ")
+
+
+def _d(B=2, T=256, C=256, H=4, N=64, T_max=None, eps=1e-6):
+    return _lib.desc(B, T, C, H, N, T if T_max is None else T_max, eps)
+
+
+def test_workspace_bytes(lib):
+    assert lib.mea_workspace_bytes(None, 0) == 0
+    assert lib.mea_workspace_bytes(ctypes.byref(_d()), 7) == 0
+    fwd = lib.mea_workspace_bytes(ctypes.byref(_d()), _lib.MEA_PASS_FWD)
+    bwd = lib.mea_workspace_bytes(ctypes.byref(_d()), _lib.MEA_PASS_BWD)
+    M, HN = 2 * 256, 4 * 64
+    assert fwd >= 5 * M * HN * 2
+    assert bwd > fwd
+    # Invalid descriptors report 0.
+    for bad in (_d(N=96), _d(C=300), _d(T_max=10), _d(eps=0.0), _d(B=0)):
+        assert lib.mea_workspace_bytes(ctypes.byref(bad), 0) == 0
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(N=32), "MEA_ERR_HEAD_DIM"),
+        (dict(C=384), "MEA_ERR_MODEL_DIM"),
+        (dict(T_max=100), "MEA_ERR_SHAPE"),
+        (dict(H=0), "MEA_ERR_SHAPE"),
+        (dict(eps=-1.0), "MEA_ERR_EPS"),
+        (dict(eps=float("nan")), "MEA_ERR_EPS"),
+    ],
+)
+def test_descriptor_validation_before_launch(lib, kw, code):
+    d = _d(**kw)
+    z = [None] * 32
+    assert lib.mea_fwd(ctypes.byref(d), *z[:12], 0, None) == _header_enum(code)
+    assert lib.mea_bwd(ctypes.byref(d), *z[:20], 0, None) == _header_enum(code)
+
+
+def test_pointer_and_workspace_validation(lib):
+    d = _d()
+    fake = 1 << 20  # aligned, never dereferenced: validation fails first
+    args = [fake] * 6 + [fake, fake, fake, fake, fake, fake]
+    assert lib.mea_fwd(ctypes.byref(d), None, *args[1:], 10, None) == _header_enum("MEA_ERR_NULL")
+    assert lib.mea_fwd(ctypes.byref(d), fake + 2, *args[1:], 10, None) == _header_enum("MEA_ERR_ALIGN")
+    # Only one of o_save / lse_save.
+    a2 = list(args)
+    a2[9] = None
+    assert lib.mea_fwd(ctypes.byref(d), fake, *a2[1:], 10, None) == _header_enum("MEA_ERR_NULL")
+    # Workspace too small.
+    assert lib.mea_fwd(ctypes.byref(d), fake, *args[1:], 10, None) == _header_enum("MEA_ERR_WORKSPACE")
+    # mea_bwd pointers: dy x wq wk wv wg wo f1 f2 o lse dx dwq dwk dwv dwg dwo df1 df2 ws
+    bargs = [fake] * 20
+    b_dwo_null = list(bargs)
+    b_dwo_null[16] = None
+    assert lib.mea_bwd(ctypes.byref(d), *b_dwo_null, 10, None) == _header_enum("MEA_ERR_NULL")
+    b_one_df = list(bargs)
+    b_one_df[18] = None
+    assert lib.mea_bwd(ctypes.byref(d), *b_one_df, 10, None) == _header_enum("MEA_ERR_NULL")
+    assert lib.mea_bwd(ctypes.byref(d), *bargs, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
+    # C > 1024 is forward-only.
+    d2 = _d(C=2048)
+    assert lib.mea_bwd(ctypes.byref(d2), *bargs, 1 << 40, None) == _header_enum("MEA_ERR_MODEL_DIM")
+
+
+def _cpu_args(B=1, T=8, C=256, H=4, N=64, dtype=torch.bfloat16):
+    HN = H * N
+    x = torch.randn(B, T, C, dtype=dtype)
+    ws = [torch.zeros(HN, C, dtype=dtype) for _ in range(4)] + [torch.zeros(C, HN, dtype=dtype)]
+    f1 = torch.ones(T, N, dtype=dtype)
+    f2 = torch.zeros(T, N, dtype=dtype)
+    return x, ws, f1, f2
+
+
+@pytest.mark.parametrize(
+    "mutate,exc",
+    [
+        (lambda a: a.update(x=a["x"].float()), TypeError),
+        (lambda a: a.update(N=32), ValueError),
+        (lambda a: a.update(H=0), ValueError),
+        (lambda a: a.update(f1=a["f1"][:4], f2=a["f2"][:4]), ValueError),
+        (lambda a: a.update(x=a["x"][:, :, :128]), ValueError),
+        (lambda a: a.update(eps=0.0), ValueError),
+        (lambda a: None, RuntimeError),  # valid shapes but on the CPU: no fallback
+    ],
+)
+def test_python_validation(mutate, exc):
+    x, ws, f1, f2 = _cpu_args()
+    a = dict(x=x, f1=f1, f2=f2, N=64, H=4, eps=1e-6)
+    mutate(a)
+    with pytest.raises(exc):
+        FusedAttentionFunction.apply(a["x"], *ws, a["f1"], a["f2"], a["H"], a["N"], a["eps"])
+
+
+def test_module_and_tables_construct_on_cpu():
+    m = CausalSoftmaxAttention(256, 4, 64)
+    assert torch.all(m.o_proj.weight == 0)
+    bound = 0.5 / 256 ** 0.5
+    assert m.q_proj.weight.abs().max() <= bound and m.q_proj.bias is None
+    y = Yarn(64, 128)
+    assert y.factor1.shape == (128, 64) and y.factor1.dtype == torch.bfloat16
+    x = torch.randn(1, 8, 256, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):  # fp32 weights of a fresh nn.Linear are rejected like the reference would
+        fused_attn(x, m.q_proj, m.k_proj, m.v_proj, m.g_proj, m.o_proj, y, 4, 64)
