@@ -121,7 +121,9 @@ __global__ __launch_bounds__(256) void dz_gate_bwd_kernel(DzParams p) {
       float dov[8], dag[8], dl = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        dov[i] = dz[i] * sg[i];
+        // delta uses the bf16-rounded dO the attention backward consumes, so
+        // dP - delta cancels exactly where it should (a single key, T = 1).
+        dov[i] = bf2f(f2bf(dz[i] * sg[i]));
         dag[i] = rxv * dz[i] * ov[i] * sg[i] * (1.0f - sg[i]);
         dl += dov[i] * ov[i];
       }
