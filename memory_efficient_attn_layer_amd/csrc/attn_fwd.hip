@@ -5,14 +5,24 @@
 // scale = 1/sqrt(N) (:426), causal, no dropout, returning the output and the
 // natural-log row normaliser (lse).
 //
-// One workgroup = one (batch, head) and BQ = 128 queries; wave w owns
-// queries 32w .. 32w+31. Keys stream through LDS in tiles of 64.
-// Scores are computed transposed, S^T = K Q^T, so that the query index sits
-// on the lane (c) and the key index on the accumulator registers: the
-// softmax statistics are then per-lane values, and the probability tile is
-// already laid out as the B operand of O^T = V^T P^T (keys 4g..4g+3 and
-// 16+4g..16+4g+3 of each 32-key step, matched by the V^T fragment reads).
-// Output is written straight into the (B, T, H*N) layout the output
+// One workgroup = one (batch, head) and BQ = 4*QW queries; wave w owns QW
+// consecutive queries (QW = 64 for N = 64, 32 for N = 128). Keys stream
+// through LDS in tiles of 64, loaded straight from global memory into a
+// swizzled row-major layout (global_load_lds, double-buffered, one barrier
+// per tile). Each tile is consumed in two 32-key steps with
+// v_mfma_f32_32x32x16_bf16:
+//   S^T = K Q^T     A = K rows from LDS, B = Q^T held in registers;
+//                   the query index sits on the lane, so every softmax
+//                   statistic is a per-lane value (plus one exchange with
+//                   lane ^ 32, which holds the other 16 keys of the step);
+//   O^T += V^T P^T  A = V^T read from the row-major V tile with the
+//                   transposing ds_read_b64_tr_b16, B = P^T straight from
+//                   the S^T accumulator registers (keys in the order the
+//                   accumulator holds them, matched by the V^T rows read).
+// The running maximum is only raised when a new score exceeds it by more
+// than 2^8 (in exp2 units); probabilities stay below 2^8, and the costly
+// rescale of the output accumulator is skipped on almost every step.
+// The output is written straight into the (B, T, H*N) layout the output
 // projection reads (the reference's gate_repack layout, :171-176).
 #include "common.cuh"
 #include "kernels.h"
@@ -20,204 +30,192 @@
 namespace mea {
 
 template <int N>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnFwdParams p) {
-  constexpr int BQ = 128, BKV = 64, QW = 32;
-  constexpr int KP = N + 8;     // K tile pitch
-  constexpr int VP = BKV + 8;   // V^T tile pitch
-  constexpr int NS = N / 32;    // MFMA k-steps over the head dim
-  constexpr int DB = N / 16;    // output d-blocks
-  constexpr int OP = N + 8;     // output staging pitch
-  constexpr int SM_LOOP = BKV * KP + N * VP, SM_OUT = 4 * QW * OP;
-  constexpr int SMEM = SM_LOOP > SM_OUT ? SM_LOOP : SM_OUT;
-  __shared__ __attribute__((aligned(16))) bf16_bits smem[SMEM];
-  bf16_bits* Ks = smem;
-  bf16_bits* Vt = smem + BKV * KP;
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
+  constexpr int QW = N == 64 ? 64 : 32;  // queries per wave
+  constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
+  constexpr int BQ = 4 * QW;             // queries per workgroup
+  constexpr int BKV = 64;                // keys per LDS tile
+  constexpr int CH = N / 8;              // 16-byte chunks per row
+  constexpr int KS = N / 16;             // MFMA k-steps over the head dim
+  constexpr int DB = N / 32;             // 32-wide output column blocks
+  constexpr int TILE = BKV * N;          // elements of one K or V tile
+  constexpr int LOADS = TILE / 8 / 256;  // 16-byte loads per thread per tile
+  constexpr float TAU = 8.f;
+  constexpr int OP = N + 8;              // output staging pitch
+  constexpr int SMEM = 4 * TILE > 4 * QW * OP ? 4 * TILE : 4 * QW * OP;
+  __shared__ __attribute__((aligned(16))) bf16_bits smem[SMEM];  // [stage][K | V], then output staging
 
-  const int T = p.T, H = p.H, BH = p.B * p.H;
+  const int T = p.T, BH = p.B * p.H;
   const int nqb = (T + BQ - 1) / BQ;
-  // Heaviest (last) query blocks first; consecutive ids walk (b, h) so all
-  // blocks of one head land on one XCD when B*H is a multiple of 8.
-  const int L = blockIdx.x;
-  const int bh = L % BH, qi = nqb - 1 - L / BH;
-  const int b = bh / H, h = bh % H;
-  const int q0 = qi * BQ;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
-  const int qw0 = q0 + wave * QW;
+  // Each XCD walks whole heads (heaviest query block of a head first), so
+  // the K/V tiles of a head are fetched once into that XCD's L2.
+  const int lid = xcd_remap(blockIdx.x, BH * nqb);
+  const int bh = lid / nqb, qi = nqb - 1 - lid % nqb;
+  const int b = bh / p.H, hd = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, h = lane >> 5;
+  const int q0w = qi * BQ + wave * QW;
+  const int kv_end = min(T, qi * BQ + BQ);
   const size_t head_off = (size_t)bh * T * N;
-  const bf16_bits* qg = p.q + head_off;
   const bf16_bits* kg = p.k + head_off;
   const bf16_bits* vg = p.v + head_off;
 
-  // Q fragments (B operand of S^T): lane holds query c of block qb, d = 32s+8g..
-  bf16x8 qf[2][NS];
+  // Q^T fragments (B operand): lane holds query q0w + 32qb + c, d = 16ks + 8h.
+  bf16x8 qf[QB][KS];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int t = qw0 + qb * 16 + c16;
+  for (int qb = 0; qb < QB; ++qb) {
+    const int t = min(q0w + 32 * qb + c, T - 1);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (t < T) v = ld16(qg + (size_t)t * N + s * 32 + 8 * g);
-      qf[qb][s] = as_frag(v);
-    }
+    for (int ks = 0; ks < KS; ++ks) qf[qb][ks] = as_frag(ld16(p.q + head_off + (size_t)t * N + 16 * ks + 8 * h));
   }
 
-  // Cooperative tile loads: K rows as 16-byte chunks, V as row pairs that are
-  // interleaved into 32-bit words of the transposed tile.
-  constexpr int KCH = BKV * N / 8 / 256;        // K chunks per thread
-  constexpr int VCH = (BKV / 2) * (N / 8) / 256;  // V row-pair chunks per thread
-  u32x4 rk[KCH], rv0[VCH], rv1[VCH];
-  auto fetch = [&](int j0) {
+  auto issue_tile = [&](int j0, int stage) {
+    bf16_bits* kt = smem + stage * 2 * TILE;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (N / 8), dc = id % (N / 8);
-      const int t = j0 + row;
-      rk[i] = t < T ? ld16(kg + (size_t)t * N + dc * 8) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int id = tid + 256 * i, rp = id / (N / 8), dc = id % (N / 8);
-      const int t = j0 + 2 * rp;
-      rv0[i] = t < T ? ld16(vg + (size_t)t * N + dc * 8) : u32x4{0u, 0u, 0u, 0u};
-      rv1[i] = t + 1 < T ? ld16(vg + (size_t)(t + 1) * N + dc * 8) : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store = [&]() {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (N / 8), dc = id % (N / 8);
-      st16(Ks + row * KP + dc * 8, rk[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int id = tid + 256 * i, rp = id / (N / 8), dc = id % (N / 8);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(Vt + (dc * 8) * VP + 2 * rp);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t a = rv0[i][e], c = rv1[i][e];
-        dst[(2 * e) * VP / 2] = (a & 0xffffu) | (c << 16);
-        dst[(2 * e + 1) * VP / 2] = (a >> 16) | (c & 0xffff0000u);
-      }
+    for (int u = 0; u < LOADS; ++u) {
+      const int slot = (u * 4 + wave) * 64 + lane;
+      const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+      const size_t off = (size_t)min(j0 + row, T - 1) * N + cc * 8;
+      g2lds16(kg + off, kt + (u * 4 + wave) * 512);
+      g2lds16(vg + off, kt + TILE + (u * 4 + wave) * 512);
     }
   };
 
-  const int kv_end = min(T, q0 + BQ);
+  float m_i[QB], l_i[QB];
+  f32x16 o[QB][DB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_i[qb] = -INFINITY;
+    l_i[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[qb][db] = zero16();
+  }
+
+  // Lane-dependent parts of the fragment addresses.
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int tr_row = 4 * h + (i16 >> 2);             // + 16*kstep + 8*t (+ 32*st)
+  const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);  // + 32*db
+
   const int nkv = (kv_end + BKV - 1) / BKV;
-  float m_i[2] = {-INFINITY, -INFINITY}, l_i[2] = {0.f, 0.f};
-  f32x4 oacc[DB][2];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) oacc[db][0] = oacc[db][1] = zero4();
-
-  fetch(0);
+  issue_tile(0, 0);
+  wait_vmcnt0();  // also retires the Q fragment loads
+  __syncthreads();
   for (int j = 0; j < nkv; ++j) {
-    store();
-    __syncthreads();
-    if (j + 1 < nkv) fetch((j + 1) * BKV);
-    const int j0 = j * BKV;
-    if (j0 <= qw0 + QW - 1) {
-      f32x4 sacc[4][2];
+    if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
+    const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
+    const bf16_bits* vs_t = ks_t + TILE;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        sacc[kb][0] = sacc[kb][1] = zero4();
+    for (int st = 0; st < 2; ++st) {
+      const int kb0 = j * BKV + st * 32;
+      if (kb0 > q0w + QW - 1) continue;  // every key of the step is in this wave's future
+      bf16x8 kf[KS];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const bf16x8 kf = as_frag(*reinterpret_cast<const u32x4*>(Ks + (kb * 16 + c16) * KP + s * 32 + 8 * g));
-          sacc[kb][0] = mfma(kf, qf[0][s], sacc[kb][0]);
-          sacc[kb][1] = mfma(kf, qf[1][s], sacc[kb][1]);
+      for (int ks = 0; ks < KS; ++ks)
+        kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + swz_off<CH>(st * 32 + c, 16 * ks + 8 * h)));
+      bf16x8 pf[QB][2];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int qb0 = q0w + 32 * qb;
+        if (kb0 > qb0 + 31) {
+          // The whole step is masked for this query block: contributes nothing.
+          pf[qb][0] = pf[qb][1] = as_frag(u32x4{0u, 0u, 0u, 0u});
+          continue;
         }
-      }
-      const bool need_mask = (j0 + BKV - 1 > qw0) || (j0 + BKV > T);
+        f32x16 s = zero16();
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const int qq = qw0 + qb * 16 + c16;
-        float mx = -INFINITY;
+        for (int ks = 0; ks < KS; ++ks) s = mfma32(kf[ks], qf[qb][ks], s);
+        const int qq = qb0 + c;
+        if (kb0 + 31 > qb0 || kb0 + 32 > T) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float v = sacc[kb][qb][r] * p.sl2e;
-            if (need_mask) {
-              const int key = j0 + kb * 16 + 4 * g + r;
-              if (key > qq || key >= T) v = -INFINITY;
-            }
-            sacc[kb][qb][r] = v;
-            mx = fmaxf(mx, v);
+          for (int i = 0; i < 16; ++i) {
+            const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (key > qq || key >= T) s[i] = -INFINITY;
           }
-        mx = max_g(mx);
-        const float mnew = fmaxf(m_i[qb], mx);
-        const float moff = mnew == -INFINITY ? 0.f : mnew;
-        const float alpha = fast_exp2(m_i[qb] - moff);
+        }
+        float mx = s[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float ms = mx * p.sl2e;
+        const bool up = ms > m_i[qb] + TAU;
+        if (__any(up)) {
+          const float mn = up ? ms : m_i[qb];
+          const float alpha = fast_exp2(m_i[qb] - mn);
+          l_i[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
+          m_i[qb] = mn;
+        }
+        const float nm = -m_i[qb];
         float ls = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float e = fast_exp2(sacc[kb][qb][r] - moff);
-            sacc[kb][qb][r] = e;
-            ls += e;
-          }
-        l_i[qb] = l_i[qb] * alpha + ls;
-        m_i[qb] = mnew;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) oacc[db][qb] *= alpha;
-      }
-      // O^T += V^T P^T over two 32-key steps.
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        bf16x8 pf[2];
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          u32x4 w;
-          w[0] = pack2(sacc[2 * s2][qb][0], sacc[2 * s2][qb][1]);
-          w[1] = pack2(sacc[2 * s2][qb][2], sacc[2 * s2][qb][3]);
-          w[2] = pack2(sacc[2 * s2 + 1][qb][0], sacc[2 * s2 + 1][qb][1]);
-          w[3] = pack2(sacc[2 * s2 + 1][qb][2], sacc[2 * s2 + 1][qb][3]);
-          pf[qb] = as_frag(w);
+        for (int i = 0; i < 16; ++i) {
+          const float e = fast_exp2(__builtin_fmaf(s[i], p.sl2e, nm));
+          s[i] = e;
+          ls += e;
         }
+        l_i[qb] += ls;
+#pragma unroll
+        for (int kst = 0; kst < 2; ++kst) {
+          u32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
+          pf[qb][kst] = as_frag(w);
+        }
+      }
+      // O^T += V^T P^T, two 16-key MFMA steps.
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16_bits* vrow = Vt + (db * 16 + c16) * VP + s2 * 32 + 4 * g;
-          const bf16x8 vf = frag_from2(*reinterpret_cast<const u32x2*>(vrow),
-                                       *reinterpret_cast<const u32x2*>(vrow + 16));
-          oacc[db][0] = mfma(vf, pf[0], oacc[db][0]);
-          oacc[db][1] = mfma(vf, pf[1], oacc[db][1]);
+          const int r = st * 32 + 16 * kst + tr_row, col = 32 * db + tr_col;
+          const bf16x8 vf = frag_from2(lds_read_tr4(vs_t + swz_off<CH>(r, col)),
+                                       lds_read_tr4(vs_t + swz_off<CH>(r + 8, col)));
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            if (kb0 > q0w + 32 * qb + 31) continue;
+            o[qb][db] = mfma32(vf, pf[qb][kst], o[qb][db]);
+          }
         }
       }
     }
+    wait_vmcnt0();
     __syncthreads();
   }
 
-  // Normalise, write lse and stage O for row-contiguous stores.
+  // Normalise, write lse and stage O^T (lane = query) as rows for 16-byte stores.
   bf16_bits* stg = smem + wave * QW * OP;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const float l = sum_g(l_i[qb]);
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-    const int qq = qw0 + qb * 16 + c16;
-    if (p.lse != nullptr && g == 0 && qq < T)
-      p.lse[(size_t)bh * T + qq] = (m_i[qb] + __log2f(l)) * kLn2;
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l = l_i[qb] + __shfl_xor(l_i[qb], 32, 64);
+    const float inv = 1.0f / l;
+    const int qq = q0w + 32 * qb + c;
+    if (p.lse != nullptr && h == 0 && qq < T) p.lse[(size_t)bh * T + qq] = (m_i[qb] + __log2f(l)) * kLn2;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const f32x4 o = oacc[db][qb] * inv;
-      u32x2 w = {pack2(o[0], o[1]), pack2(o[2], o[3])};
-      *reinterpret_cast<u32x2*>(stg + (qb * 16 + c16) * OP + db * 16 + 4 * g) = w;
-    }
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x16& a = o[qb][db];
+        const u32x2 w = {pack2(a[4 * r4] * inv, a[4 * r4 + 1] * inv), pack2(a[4 * r4 + 2] * inv, a[4 * r4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(stg + (32 * qb + c) * OP + 32 * db + 8 * r4 + 4 * h) = w;
+      }
   }
   __syncthreads();
-  constexpr int CPR = N / 8;
-  const size_t HN = (size_t)H * N;
+  const size_t HN = (size_t)p.H * N;
 #pragma unroll
-  for (int it = 0; it < QW * CPR / 64; ++it) {
-    const int id = lane + 64 * it, row = id / CPR, dc = id % CPR;
-    const int t = qw0 + row;
+  for (int it = 0; it < QW * CH / 64; ++it) {
+    const int id = lane + 64 * it, row = id / CH, dc = id % CH;
+    const int t = q0w + row;
     if (t < T) {
       const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * OP + dc * 8);
-      st16(p.o + ((size_t)b * T + t) * HN + (size_t)h * N + dc * 8, val);
+      st16(p.o + ((size_t)b * T + t) * HN + (size_t)hd * N + dc * 8, val);
     }
   }
 }
 
 hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s) {
-  const int G = p.B * p.H * ((p.T + 127) / 128);
+  const int BQ = N == 64 ? 256 : 128;
+  const int G = p.B * p.H * ((p.T + BQ - 1) / BQ);
   if (N == 64)
     hipLaunchKernelGGL(attn_fwd_kernel<64>, dim3(G), dim3(256), 0, s, p);
   else

@@ -31,6 +31,53 @@ __device__ __forceinline__ f32x4 mfma(const bf16x8& a, const bf16x8& b, const f3
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// v_mfma_f32_32x32x16_bf16, lane = 32*h + c (h in 0..1, c in 0..31):
+//   A operand (32 rows x 16 k): lane holds row c, k = 8h .. 8h+7
+//   B operand (16 k x 32 cols): lane holds col c, k = 8h .. 8h+7
+//   D (32 x 32 fp32, 16 regs):  reg i of lane holds row 8*(i/4) + 4h + i%4, col c
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// LDS pointer types for the gfx950 LDS-only instructions.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane 4a+b receives
+// element b of the 4-element rows addressed by lanes a, 4+a, 8+a, 12+a (in
+// that order). With lane i of the group addressing row r0 + (i >> 2),
+// column c0 + 4*(i & 3) of a row-major bf16 matrix, lane j gets column
+// c0 + j of rows r0 .. r0+3: a k-major MFMA operand read from a tile whose
+// rows run along k.
+__device__ __forceinline__ u32x2 lds_read_tr4(const bf16_bits* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// global_load_lds_dwordx4: lane L copies 16 bytes from its own global
+// address to lds_wave_base + 16*L (lds_wave_base must be wave-uniform).
+// Completion is tracked by vmcnt only: the caller waits with wait_vmcnt0()
+// before the barrier that publishes the tile. Issued as inline asm so the
+// compiler does not guard every later LDS read (it cannot tell the tile
+// being filled from the one being read) with a wait for all of these loads.
+// The kernels that use it set m0 nowhere else.
+__device__ __forceinline__ void g2lds16(const void* gsrc, bf16_bits* lds_wave_base) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)((lds_void*)lds_wave_base));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gsrc), "s"(lds) : "memory");
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left open), as a builtin so the
+// compiler's own wait tracking also sees every earlier vector load retired.
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // bf16 bit patterns <-> fp32.
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -101,6 +148,21 @@ __device__ __forceinline__ float max_g(float v) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float sigmoidf(float a) { return 1.0f / (1.0f + __expf(-a)); }
+
+// Row-major bf16 tiles in LDS are stored as 16-byte chunks; chunk c of row r
+// sits at chunk slot c ^ swz(r) of that row. For rows of 8 chunks (128 B)
+// two rows share one 256-byte bank line, so 16 consecutive rows read at one
+// chunk index hit 16 distinct 16-byte bank groups; likewise for 16-chunk rows.
+template <int CH>
+__device__ __forceinline__ int chunk_swz(int row) {
+  static_assert(CH == 8 || CH == 16, "rows of 64 or 128 bf16");
+  return CH == 8 ? ((row >> 1) & 7) : (row & 15);
+}
+// Element offset of (row, col) in a swizzled tile with CH chunks per row.
+template <int CH>
+__device__ __forceinline__ int swz_off(int row, int col) {
+  return row * (CH * 8) + (((col >> 3) ^ chunk_swz<CH>(row)) << 3) + (col & 7);
+}
 
 // Block-id remapping so that consecutive logical tiles run on the same XCD.
 // The hardware hands workgroup L to XCD L % 8; logical tile ids
