@@ -21,6 +21,8 @@
 //                 S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
 // Operands that reduce over a sequence index (K^T, Q^T, dO^T) are written
 // into LDS transposed, as 32-bit pairs of adjacent rows.
+#include <type_traits>
+
 #include "common.cuh"
 #include "kernels.h"
 
@@ -264,186 +266,217 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdParams p) {
 
 // ---------------------------------------------------------------------------
 // dK, dV
+//
+// One workgroup = one (batch, head) and BKV = 4*KW keys; wave w owns KW
+// consecutive keys (KW = 64 for N = 64, 32 for N = 128) whose K and V rows
+// stay in registers as the B operands of
+//   S  = Q K^T   and   dP = dO V^T        (A = Q, dO rows from LDS)
+// on v_mfma_f32_32x32x16_bf16. The key index sits on the lane, so P and
+// dS = P (dP - delta) are already the B operands (k = query) of
+//   dV^T += dO^T P   and   dK^T += Q^T dS
+// whose A operands dO^T, Q^T are read from the same row-major LDS tiles with
+// the transposing ds_read_b64_tr_b16. Query tiles of 64 stream through LDS
+// (global_load_lds, double-buffered, one barrier per tile), starting at the
+// block's first key (causal).
 // ---------------------------------------------------------------------------
 template <int N>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
-  constexpr int BKV = 128, KW = 32, BQ = 64;
-  constexpr int QP = N + 8, TP = BQ + 8;
-  constexpr int NS = N / 32, DB = N / 16, FP = N + 4;
-  constexpr int SM_LOOP = (2 * BQ * QP + 2 * N * TP) * 2 + 2 * BQ * 4;
-  constexpr int SM_OUT = 4 * KW * FP * 4;
+  constexpr int KW = N == 64 ? 64 : 32;  // keys per wave
+  constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
+  constexpr int BKV = 4 * KW;            // keys per workgroup
+  constexpr int BQ = 64;                 // queries per LDS tile
+  constexpr int CH = N / 8, KS = N / 16, DB = N / 32;
+  constexpr int TILE = BQ * N;
+  constexpr int LOADS = TILE / 8 / 256;
+  constexpr int FP = N + 4;  // fp32 staging pitch
+  constexpr int SM_LOOP = 2 * 2 * TILE * 2 + 2 * 2 * BQ * 4;  // bytes
+  constexpr int SM_OUT = 4 * 32 * FP * 4;
   constexpr int SMEM = SM_LOOP > SM_OUT ? SM_LOOP : SM_OUT;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
-  bf16_bits* Qs = reinterpret_cast<bf16_bits*>(smem);
-  bf16_bits* Ds = Qs + BQ * QP;
-  bf16_bits* Qt = Ds + BQ * QP;
-  bf16_bits* Dt = Qt + N * TP;
-  float* lse_s = reinterpret_cast<float*>(Dt + N * TP);
-  float* dlt_s = lse_s + BQ;
+  bf16_bits* tiles = reinterpret_cast<bf16_bits*>(smem);           // [stage][Q | dO]
+  float* stats = reinterpret_cast<float*>(smem + 2 * 2 * TILE * 2);  // [stage][lse*log2e | delta]
 
-  const int T = p.T, H = p.H, BH = p.B * p.H;
+  const int T = p.T, BH = p.B * p.H;
   const int nkb = (T + BKV - 1) / BKV;
-  // Key blocks near the start of the sequence see the most queries: first.
-  const int L = blockIdx.x;
-  const int bh = L % BH, ki = L / BH;
-  const int b = bh / H, h = bh % H;
-  const int k0 = ki * BKV;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
-  const int kw0 = k0 + wave * KW;
+  // Each XCD walks whole heads, the key block that sees the most queries
+  // first, so the Q/dO tiles of a head are shared in one L2.
+  const int lid = xcd_remap(blockIdx.x, BH * nkb);
+  const int bh = lid / nkb, ki = lid % nkb;
+  const int b = bh / p.H, hd = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, h = lane >> 5;
+  const int k0 = ki * BKV, kw0 = k0 + wave * KW;
   const size_t head_off = (size_t)bh * T * N;
   const bf16_bits* qg = p.q + head_off;
   const bf16_bits* dg = p.dO + head_off;
-  (void)nkb;
 
-  bf16x8 kf[2][NS], vf[2][NS];
+  // K^T, V^T fragments (B operands): lane holds key kw0 + 32kb + c, d = 16ks + 8h.
+  bf16x8 kf[KB][KS], vf[KB][KS];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    const int t = kw0 + kb * 16 + c16;
-    const bool ok = t < T;
+  for (int kb = 0; kb < KB; ++kb) {
+    const size_t row = head_off + (size_t)min(kw0 + 32 * kb + c, T - 1) * N;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const size_t off = head_off + (size_t)t * N + s * 32 + 8 * g;
-      kf[kb][s] = as_frag(ok ? ld16(p.k + off) : u32x4{0u, 0u, 0u, 0u});
-      vf[kb][s] = as_frag(ok ? ld16(p.v + off) : u32x4{0u, 0u, 0u, 0u});
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[kb][ks] = as_frag(ld16(p.k + row + 16 * ks + 8 * h));
+      vf[kb][ks] = as_frag(ld16(p.v + row + 16 * ks + 8 * h));
     }
   }
 
-  constexpr int PCH = (BQ / 2) * (N / 8) / 256;  // row-pair chunks per thread
-  u32x4 rq0[PCH], rq1[PCH], rd0[PCH], rd1[PCH];
-  float rstat = 0.f;
-  auto fetch = [&](int i0) {
+  float st_reg = 0.f;
+  auto issue_tile = [&](int q0, int stage) {
+    bf16_bits* qt = tiles + stage * 2 * TILE;
 #pragma unroll
-    for (int i = 0; i < PCH; ++i) {
-      const int id = tid + 256 * i, rp = id / (N / 8), dc = id % (N / 8);
-      const int t = i0 + 2 * rp;
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      rq0[i] = t < T ? ld16(qg + (size_t)t * N + dc * 8) : z;
-      rq1[i] = t + 1 < T ? ld16(qg + (size_t)(t + 1) * N + dc * 8) : z;
-      rd0[i] = t < T ? ld16(dg + (size_t)t * N + dc * 8) : z;
-      rd1[i] = t + 1 < T ? ld16(dg + (size_t)(t + 1) * N + dc * 8) : z;
+    for (int u = 0; u < LOADS; ++u) {
+      const int slot = (u * 4 + wave) * 64 + lane;
+      const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+      const size_t off = (size_t)min(q0 + row, T - 1) * N + cc * 8;
+      g2lds16(qg + off, qt + (u * 4 + wave) * 512);
+      g2lds16(dg + off, qt + TILE + (u * 4 + wave) * 512);
     }
     if (tid < 2 * BQ) {
-      const int t = i0 + (tid & (BQ - 1));
-      rstat = t < T ? (tid < BQ ? p.lse[(size_t)bh * T + t] * kLog2e : p.delta[(size_t)bh * T + t]) : 0.f;
+      const size_t t = (size_t)bh * T + min(q0 + (tid & (BQ - 1)), T - 1);
+      st_reg = tid < BQ ? p.lse[t] : p.delta[t];
     }
   };
-  auto store = [&]() {
+  // Called after wait_vmcnt0(): st_reg is consumed only once every load of
+  // the tile has landed, so no wait is placed inside the prefetch.
+  auto publish_stats = [&](int stage) {
+    if (tid < 2 * BQ) stats[stage * 2 * BQ + tid] = tid < BQ ? st_reg * kLog2e : st_reg;
+  };
+
+  f32x16 dv[KB][DB], dk[KB][DB];
 #pragma unroll
-    for (int i = 0; i < PCH; ++i) {
-      const int id = tid + 256 * i, rp = id / (N / 8), dc = id % (N / 8);
-      st16(Qs + (2 * rp) * QP + dc * 8, rq0[i]);
-      st16(Qs + (2 * rp + 1) * QP + dc * 8, rq1[i]);
-      st16(Ds + (2 * rp) * QP + dc * 8, rd0[i]);
-      st16(Ds + (2 * rp + 1) * QP + dc * 8, rd1[i]);
-      uint32_t* dq_ = reinterpret_cast<uint32_t*>(Qt + (dc * 8) * TP + 2 * rp);
-      uint32_t* dd_ = reinterpret_cast<uint32_t*>(Dt + (dc * 8) * TP + 2 * rp);
+  for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint32_t a = rq0[i][e], c = rq1[i][e];
-        dq_[(2 * e) * TP / 2] = (a & 0xffffu) | (c << 16);
-        dq_[(2 * e + 1) * TP / 2] = (a >> 16) | (c & 0xffff0000u);
-        a = rd0[i][e];
-        c = rd1[i][e];
-        dd_[(2 * e) * TP / 2] = (a & 0xffffu) | (c << 16);
-        dd_[(2 * e + 1) * TP / 2] = (a >> 16) | (c & 0xffff0000u);
+    for (int db = 0; db < DB; ++db) dv[kb][db] = dk[kb][db] = zero16();
+
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int tr_row = 4 * h + (i16 >> 2);
+  const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+
+  const int nq = (T - k0 + BQ - 1) / BQ;
+  issue_tile(k0, 0);
+  wait_vmcnt0();
+  publish_stats(0);
+  __syncthreads();
+  for (int it = 0; it < nq; ++it) {
+    const int q0 = k0 + it * BQ;
+    if (it + 1 < nq) issue_tile(q0 + BQ, (it + 1) & 1);
+    const bf16_bits* qt = tiles + (it & 1) * 2 * TILE;
+    const bf16_bits* dt = qt + TILE;
+    const float* ls = stats + (it & 1) * 2 * BQ;
+    const float* dls = ls + BQ;
+    // One 32-query step; DIAG steps mask key > query and query >= T with
+    // selects, the others run without any per-element test. Each variant is
+    // one basic block, so the scheduler can overlap the MFMAs of one key
+    // block with the exp/convert work of the other.
+    auto step = [&](int sub, auto diag_tag) {
+      constexpr bool DIAG = decltype(diag_tag)::value;
+      const int qs0 = q0 + 32 * sub;
+      bf16x8 qa[KS], da[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = swz_off<CH>(32 * sub + c, 16 * ks + 8 * h);
+        qa[ks] = as_frag(*reinterpret_cast<const u32x4*>(qt + off));
+        da[ks] = as_frag(*reinterpret_cast<const u32x4*>(dt + off));
       }
-    }
-    if (tid < 2 * BQ) lse_s[tid] = rstat;  // lse_s and dlt_s are contiguous
-  };
-
-  f32x4 dk[DB][2], dv[DB][2];
+      // Statistics of the queries held by accumulator register 4*r4 + e:
+      // query qs0 + 8*r4 + 4h + e.
+      f32x4 l4[4], d4[4];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) dk[db][0] = dk[db][1] = dv[db][0] = dv[db][1] = zero4();
-
-  const int nq = k0 < T ? (T - k0 + BQ - 1) / BQ : 0;
-  if (nq > 0) fetch(k0);
-  for (int i = 0; i < nq; ++i) {
-    store();
-    __syncthreads();
-    const int i0 = k0 + i * BQ;
-    if (i + 1 < nq) fetch(i0 + BQ);
-    if (i0 + BQ - 1 >= kw0) {
-      f32x4 sa[4][2], pa[4][2];
+      for (int r4 = 0; r4 < 4; ++r4) {
+        l4[r4] = *reinterpret_cast<const f32x4*>(ls + 32 * sub + 8 * r4 + 4 * h);
+        d4[r4] = *reinterpret_cast<const f32x4*>(dls + 32 * sub + 8 * r4 + 4 * h);
+      }
+      bf16x8 pb[KB][2], sb[KB][2];
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
-        sa[qb][0] = sa[qb][1] = pa[qb][0] = pa[qb][1] = zero4();
+      for (int kb = 0; kb < KB; ++kb) {
+        f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const bf16x8 qa = as_frag(*reinterpret_cast<const u32x4*>(Qs + (qb * 16 + c16) * QP + s * 32 + 8 * g));
-          const bf16x8 da = as_frag(*reinterpret_cast<const u32x4*>(Ds + (qb * 16 + c16) * QP + s * 32 + 8 * g));
-          sa[qb][0] = mfma(qa, kf[0][s], sa[qb][0]);
-          sa[qb][1] = mfma(qa, kf[1][s], sa[qb][1]);
-          pa[qb][0] = mfma(da, vf[0][s], pa[qb][0]);
-          pa[qb][1] = mfma(da, vf[1][s], pa[qb][1]);
+        for (int ks = 0; ks < KS; ++ks) {
+          s = mfma32(qa[ks], kf[kb][ks], s);
+          dp = mfma32(da[ks], vf[kb][ks], dp);
         }
-      }
-      // sa <- P, pa <- dS.
+        const int key = kw0 + 32 * kb + c;
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int ql = qb * 16 + 4 * g + r;
-          const int qq = i0 + ql;
-          const float l2 = lse_s[ql], dl = dlt_s[ql];
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            const int key = kw0 + kb * 16 + c16;
-            float pv = fast_exp2(sa[qb][kb][r] * p.sl2e - l2);
-            if (key > qq || qq >= T) pv = 0.f;
-            sa[qb][kb][r] = pv;
-            pa[qb][kb][r] = pv * (pa[qb][kb][r] - dl);
+        for (int i = 0; i < 16; ++i) {
+          const int r4 = i >> 2, e = i & 3;
+          float pv = fast_exp2(__builtin_fmaf(s[i], p.sl2e, -l4[r4][e]));
+          if (DIAG) {
+            const int q = qs0 + 8 * r4 + 4 * h + e;
+            pv = (key > q || q >= T) ? 0.f : pv;
           }
+          s[i] = pv;
+          dp[i] = pv * (dp[i] - d4[r4][e]);
         }
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        bf16x8 pf[2], sf[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kst = 0; kst < 2; ++kst) {
           u32x4 w, u;
-          w[0] = pack2(sa[2 * s2][kb][0], sa[2 * s2][kb][1]);
-          w[1] = pack2(sa[2 * s2][kb][2], sa[2 * s2][kb][3]);
-          w[2] = pack2(sa[2 * s2 + 1][kb][0], sa[2 * s2 + 1][kb][1]);
-          w[3] = pack2(sa[2 * s2 + 1][kb][2], sa[2 * s2 + 1][kb][3]);
-          u[0] = pack2(pa[2 * s2][kb][0], pa[2 * s2][kb][1]);
-          u[1] = pack2(pa[2 * s2][kb][2], pa[2 * s2][kb][3]);
-          u[2] = pack2(pa[2 * s2 + 1][kb][0], pa[2 * s2 + 1][kb][1]);
-          u[3] = pack2(pa[2 * s2 + 1][kb][2], pa[2 * s2 + 1][kb][3]);
-          pf[kb] = as_frag(w);
-          sf[kb] = as_frag(u);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
+            u[e] = pack2(dp[8 * kst + 2 * e], dp[8 * kst + 2 * e + 1]);
+          }
+          pb[kb][kst] = as_frag(w);
+          sb[kb][kst] = as_frag(u);
         }
+      }
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16_bits* dr = Dt + (db * 16 + c16) * TP + s2 * 32 + 4 * g;
-          const bf16_bits* qr = Qt + (db * 16 + c16) * TP + s2 * 32 + 4 * g;
-          const bf16x8 dt = frag_from2(*reinterpret_cast<const u32x2*>(dr), *reinterpret_cast<const u32x2*>(dr + 16));
-          const bf16x8 qt = frag_from2(*reinterpret_cast<const u32x2*>(qr), *reinterpret_cast<const u32x2*>(qr + 16));
-          dv[db][0] = mfma(dt, pf[0], dv[db][0]);
-          dv[db][1] = mfma(dt, pf[1], dv[db][1]);
-          dk[db][0] = mfma(qt, sf[0], dk[db][0]);
-          dk[db][1] = mfma(qt, sf[1], dk[db][1]);
+          const int r = 32 * sub + 16 * kst + tr_row, col = 32 * db + tr_col;
+          const int o0 = swz_off<CH>(r, col), o1 = swz_off<CH>(r + 8, col);
+          const bf16x8 dT = frag_from2(lds_read_tr4(dt + o0), lds_read_tr4(dt + o1));
+          const bf16x8 qT = frag_from2(lds_read_tr4(qt + o0), lds_read_tr4(qt + o1));
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            dv[kb][db] = mfma32(dT, pb[kb][kst], dv[kb][db]);
+            dk[kb][db] = mfma32(qT, sb[kb][kst], dk[kb][db]);
+          }
         }
       }
+    };
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int qs0 = q0 + 32 * sub;
+      if (qs0 + 31 < kw0 || qs0 >= T) continue;  // wave-uniform: nothing to add
+      if (qs0 < kw0 + KW - 1 || qs0 + 31 >= T)
+        step(sub, std::true_type{});
+      else
+        step(sub, std::false_type{});
     }
+    wait_vmcnt0();
+    if (it + 1 < nq) publish_stats((it + 1) & 1);
     __syncthreads();
   }
 
-  // dV tail, then dK tail (shared staging).
-  float* stg = reinterpret_cast<float*>(smem) + wave * KW * FP;
+  // Epilogue per 32-key block: stage dV (then dK * scale) as fp32 rows and run
+  // the row-wise tails (rx scale; k RMSNorm + rotary backward for dK).
+  float* stg = reinterpret_cast<float*>(smem) + wave * 32 * FP;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-      *reinterpret_cast<f32x4*>(stg + (kb * 16 + c16) * FP + db * 16 + 4 * g) = dv[db][kb];
-  __syncthreads();
-  head_row_bwd<N>(stg, FP, kw0, p, b, h, false, nullptr, nullptr, p.dav);
-  __syncthreads();
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+  for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
     for (int db = 0; db < DB; ++db)
-      *reinterpret_cast<f32x4*>(stg + (kb * 16 + c16) * FP + db * 16 + 4 * g) = dk[db][kb] * p.scale;
-  __syncthreads();
-  head_row_bwd<N>(stg, FP, kw0, p, b, h, true, p.k, p.rk, p.dak);
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x4 v = {dv[kb][db][4 * r4], dv[kb][db][4 * r4 + 1], dv[kb][db][4 * r4 + 2], dv[kb][db][4 * r4 + 3]};
+        *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v;
+      }
+    __syncthreads();
+    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, b, hd, false, nullptr, nullptr, p.dav);
+    __syncthreads();
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x4 v = {dk[kb][db][4 * r4], dk[kb][db][4 * r4 + 1], dk[kb][db][4 * r4 + 2], dk[kb][db][4 * r4 + 3]};
+        *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v * p.scale;
+      }
+    __syncthreads();
+    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, b, hd, true, p.k, p.rk, p.dak);
+    __syncthreads();
+  }
 }
 
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
@@ -456,7 +489,8 @@ hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
 }
 
 hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s) {
-  const int G = p.B * p.H * ((p.T + 127) / 128);
+  const int BKV = N == 64 ? 256 : 128;
+  const int G = p.B * p.H * ((p.T + BKV - 1) / BKV);
   if (N == 64)
     hipLaunchKernelGGL(attn_bwd_dkdv_kernel<64>, dim3(G), dim3(256), 0, s, p);
   else
