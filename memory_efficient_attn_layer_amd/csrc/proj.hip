@@ -5,174 +5,202 @@
 // fused_qkvg_norm_rope_kernel (:36-144), and their backward-recompute
 // variants (:181-332) when rx/rq/rk are requested.
 //
-// Tile: one workgroup owns BM = 8192/N token rows and one head h; its four
-// waves compute the four projections of that head (wave p -> W_p rows
-// h*N .. h*N+N-1), so every head-local reduction of the epilogue stays inside
-// one wave. The input RMSNorm is never materialised: diag(1/rms(x)) commutes
-// with the GEMM, so each thread accumulates the sum of squares of the x
-// chunks it streams and the row scale is applied to the fp32 accumulator.
-#include "gemm_core.cuh"
+// The product is computed transposed, D^T = W x^T: the A operand is a slice
+// of the stacked weights [Wq_h; Wk_h; Wv_h; Wg_h] of one head h (features),
+// the B operand a tile of x rows (tokens). In the 16x16 accumulator layout a
+// lane then holds one token and 4 consecutive features, so the head RMSNorm
+// is an in-lane sum plus two lane exchanges, both members of every rotary
+// pair (n, n^1) sit in one lane, and results leave as 8-byte stores.
+//
+// Tile: 256 features x 256 tokens, k-slabs of 64 double-buffered in LDS and
+// filled by direct global->LDS loads (one barrier per slab). Four waves, each
+// 128 features x 128 tokens (64 accumulators of 16x16).
+//
+// The input RMSNorm is never materialised: diag(1/rms(x)) commutes with the
+// GEMM. The waves sum the squares of the x fragments they read anyway (the two
+// waves sharing a token half split the rows) and the row scale multiplies the
+// fp32 accumulator.
 #include "kernels.h"
+#include "slab.cuh"
 
 namespace mea {
 
 template <int N>
-__global__ __launch_bounds__(256) void qkvg_proj_kernel(ProjParams p) {
-  constexpr int BM = 8192 / N, BN = 4 * N;
-  constexpr int MB = BM / 16, NB = N / 16;
-  constexpr int SP = N + 8;  // staging pitch (elements)
-  constexpr int SMEM_MAIN = NtSmem<BM, BN>::elems, SMEM_STG = 4 * BM * SP;
-  constexpr int SMEM = SMEM_MAIN > SMEM_STG ? SMEM_MAIN : SMEM_STG;
-  __shared__ __attribute__((aligned(16))) bf16_bits smem[SMEM];
-  __shared__ float rxs[BM];
-
-  const int M = p.M, C = p.C, H = p.H, T = p.T, HN = H * N;
-  const int ntm = (M + BM - 1) / BM;
-  const int L = xcd_remap(blockIdx.x, ntm * H);
-  const int h = L % H, m0 = (L / H) * BM;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
+__global__ __launch_bounds__(256, 1) void qkvg_proj_kernel(ProjParams p) {
+  constexpr int BT = 256;              // tokens per tile
+  constexpr int BF = 256;              // stacked-weight rows per tile
+  constexpr int NFT = 4 * N / BF;      // feature tiles per head
+  constexpr int STAGE = (BF + BT) * kSlabK;
+  constexpr int GF = N / 16;           // 16-feature blocks per projection
+  constexpr int NG = 8 / GF;           // projections per wave
+  __shared__ __attribute__((aligned(16))) bf16_bits smem[2 * STAGE];
+  __shared__ float ssq_s[BT];
 
   // Locals, not captures of the argument block: a lambda holding &p would
   // force the block into scratch memory.
   const bf16_bits* __restrict__ xg = p.x;
   const bf16_bits *wq = p.wq, *wk = p.wk, *wv = p.wv, *wg = p.wg;
-  bf16_bits *oq = p.q, *ok = p.k, *ov = p.v, *osig = p.sig;
-  float *rq = p.rq, *rk = p.rk;
+  const int M = p.M, C = p.C, H = p.H, T = p.T, HN = H * N;
 
-  // Sum of squares of the x rows this thread streams: rows (tid>>2) + 64*i.
-  float ss0 = 0.f, ss1 = 0.f;
-  auto load_a = [&](int row, int k0, int kc, int) -> u32x4 {
-    const int m = m0 + row;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (m < M) {
-      v = ld16(xg + (size_t)m * C + k0 + kc * 8);
-      float f[8];
-      unpack8(v, f);
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s += f[i] * f[i];
-      if (row >= 64) ss1 += s; else ss0 += s;
-    }
-    return v;
+  const int ntt = (M + BT - 1) / BT;
+  const int L = xcd_remap(blockIdx.x, ntt * H * NFT);
+  const int tt = L / (H * NFT), rem = L - tt * (H * NFT);
+  const int h = rem / NFT, f0 = (rem % NFT) * BF;
+  const int m0 = tt * BT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
+  const int wf = wave >> 1, wt = wave & 1;
+
+  // Source matrix of each N-row segment of the stacked-weight slab.
+  constexpr int NSEG = BF / N;
+  const bf16_bits* wseg[NSEG];
+  if (NSEG == 4) {
+    wseg[0] = wq;
+    wseg[NSEG > 1 ? 1 : 0] = wk;
+    wseg[NSEG > 2 ? 2 : 0] = wv;
+    wseg[NSEG > 3 ? 3 : 0] = wg;
+  } else {
+    wseg[0] = f0 == 0 ? wq : wv;
+    wseg[NSEG > 1 ? 1 : 0] = f0 == 0 ? wk : wg;
+  }
+
+  auto issue = [&](int ks, int st) {
+    bf16_bits* base = smem + st * STAGE;
+    const int k0 = ks * kSlabK;
+    slab_issue<BF>(base, [&](int r, int u) {
+      const int seg = (32 * u) / N;  // compile-time after unrolling
+      return wseg[seg] + (size_t)(h * N + r - seg * N) * C + k0;
+    });
+    slab_issue<BT>(base + BF * kSlabK, [&](int r, int) { return xg + (size_t)min(m0 + r, M - 1) * C + k0; });
   };
-  auto load_b = [&](int row, int k0, int kc, int i) -> u32x4 {
-    const int pj = (64 * i) / N, n = row % N;  // row = (tid >> 2) + 64 i
-    const bf16_bits* w = pj == 0 ? wq : pj == 1 ? wk : pj == 2 ? wv : wg;
-    return ld16(w + (size_t)(h * N + n) * C + k0 + kc * 8);
-  };
 
-  f32x4 acc[MB][NB];
-  mainloop_nt<BM, BN, 1, 4>(C, smem, load_a, load_b, acc);
-
-  // Row scale 1/rms(x): reduce over the 4 threads that share a row.
-  {
-    constexpr int ASL = (BM * 4 + 255) / 256;
+  f32x4 acc[8][8];
 #pragma unroll
-    for (int i = 0; i < ASL; ++i) {
-      float s = i == 0 ? ss0 : ss1;
-      s += xor1(s);
-      s += xor2(s);
-      const int row = (tid >> 2) + 64 * i;
-      if ((tid & 3) == 0 && row < BM) {
-        const float r = rsqrtf(s / (float)C + p.eps);
-        rxs[row] = r;
-        if (p.rx != nullptr && h == 0 && m0 + row < M) p.rx[m0 + row] = r;
+  for (int fb = 0; fb < 8; ++fb)
+#pragma unroll
+    for (int tb = 0; tb < 8; ++tb) acc[fb][tb] = zero4();
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+
+  const int nk = C / kSlabK;
+  issue(0, 0);
+  for (int ks = 0; ks < nk; ++ks) {
+    wait_vmcnt0();
+    __syncthreads();
+    if (ks + 1 < nk) issue(ks + 1, (ks + 1) & 1);
+    const bf16_bits* As = smem + (ks & 1) * STAGE;
+    const bf16_bits* Bs = As + BF * kSlabK;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 af[8], bfr[8];
+#pragma unroll
+      for (int fb = 0; fb < 8; ++fb) af[fb] = as_frag(slab_read(As, wf * 128 + fb * 16 + c16, 4 * kk + g));
+#pragma unroll
+      for (int tb = 0; tb < 8; ++tb) {
+        const u32x4 v = slab_read(Bs, wt * 128 + tb * 16 + c16, 4 * kk + g);
+        bfr[tb] = as_frag(v);
+        if ((tb >> 2) == wf) ss[tb & 3] = sumsq8(v, ss[tb & 3]);
       }
+#pragma unroll
+      for (int fb = 0; fb < 8; ++fb)
+#pragma unroll
+        for (int tb = 0; tb < 8; ++tb) acc[fb][tb] = mfma(af[fb], bfr[tb], acc[fb][tb]);
     }
+  }
+
+  // Sum of squares of each token row: lane (g, c16) holds the k chunks g and
+  // 4+g of every slab.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float s = ss[i];
+    s += shfl_xor(s, 16);
+    s += shfl_xor(s, 32);
+    if (g == 0) ssq_s[wt * 128 + (4 * wf + i) * 16 + c16] = s;
   }
   __syncthreads();
 
-  float rxv[MB][4];
+  int mrow[8];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int tb = 0; tb < 8; ++tb) {
+    const int tl = wt * 128 + tb * 16 + c16;
+    mrow[tb] = m0 + tl;
+    const float rx = rsqrtf(ssq_s[tl] / (float)C + p.eps);
+    if (p.rx != nullptr && h == 0 && f0 == 0 && wf == 0 && g == 0 && mrow[tb] < M) p.rx[mrow[tb]] = rx;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) rxv[mb][r] = rxs[mb * 16 + 4 * g + r];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[mb][nb][r] *= rxv[mb][r];
+    for (int fb = 0; fb < 8; ++fb) acc[fb][tb] *= rx;
+  }
 
-  if (wave < 2) {
-    // Head RMSNorm over N (fast_triton_attn.py:102-106). The rotary is applied
-    // in the row-contiguous store below, from the bf16-rounded normalised
-    // values, the same rounding point as the reference (:103, :140).
-    float* rstat = wave == 0 ? rq : rk;
+  const int v0 = f0 + wf * 128;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+  for (int gi = 0; gi < NG; ++gi) {
+    const int pj = v0 / N + gi;  // projection of this group (wave-uniform)
+    if (pj < 2) {
+      // Head RMSNorm over N (fast_triton_attn.py:102-106), then the rotary
+      // from the bf16-rounded normalised values, the reference's rounding
+      // point (:103, :140): out[n] = qh[n] f1[t,n] + qh[n^1] f2[t,n].
+      float* rstat = pj == 0 ? p.rq : p.rk;
+      bf16_bits* outp = pj == 0 ? p.q : p.k;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int tb = 0; tb < 8; ++tb) {
         float s = 0.f;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) s += acc[mb][nb][r] * acc[mb][nb][r];
-        s = sum16(s);
+        for (int j = 0; j < GF; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s += acc[gi * GF + j][tb][r] * acc[gi * GF + j][tb][r];
+        s += shfl_xor(s, 16);
+        s += shfl_xor(s, 32);
         const float rr = rsqrtf(s / (float)N + p.eps);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[mb][nb][r] *= rr;
-        const int m = m0 + mb * 16 + 4 * g + r;
-        if (rstat != nullptr && c16 == 0 && m < M) {
+        const int m = mrow[tb];
+        if (m < M) {
           const int b = m / T, t = m - b * T;
-          rstat[((size_t)b * H + h) * T + t] = rr;
-        }
-      }
-  } else if (wave == 3) {
+          const size_t hrow = ((size_t)b * H + h) * T + t;
+          if (rstat != nullptr && g == 0) rstat[hrow] = rr;
+          const float* f1r = p.f1 + (size_t)t * N;
+          const float* f2r = p.f2 + (size_t)t * N;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+          for (int j = 0; j < GF; ++j) {
+            const int n = 16 * j + 4 * g;
+            const f32x4 a1 = *reinterpret_cast<const f32x4*>(f1r + n);
+            const f32x4 a2 = *reinterpret_cast<const f32x4*>(f2r + n);
+            float qh[4], o[4];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+            for (int r = 0; r < 4; ++r) qh[r] = bf2f(f2bf(acc[gi * GF + j][tb][r] * rr));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mb][nb][r] = sigmoidf(acc[mb][nb][r]);
-  }
-
-  // Stage the wave's BM x N tile as bf16 and store it with 16-byte rows.
-  bf16_bits* stg = smem + wave * BM * SP;
-  stage_acc_bf16<MB, NB, SP>(stg, 0, 0, acc, [](int, int, float v) { return v; });
-  __syncthreads();
-  constexpr int CPR = N / 8;  // 16-byte chunks per row
-  bf16_bits* base = wave == 0 ? oq : wave == 1 ? ok : wave == 2 ? ov : osig;
-#pragma unroll 4
-  for (int it = 0; it < BM * CPR / 64; ++it) {
-    const int id = lane + 64 * it, row = id / CPR, dc = id % CPR;
-    const int m = m0 + row;
-    if (m < M) {
-      u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * SP + dc * 8);
-      size_t off;
-      if (wave < 3) {
-        const int b = m / T, t = m - b * T;
-        off = (((size_t)b * H + h) * T + t) * N + dc * 8;
-        if (wave < 2) {
-          // Adjacent-pair rotary out[n] = t[n]*f1[t,n] + t[n^1]*f2[t,n]
-          // (fast_triton_attn.py:132-141); both pair members are in this chunk.
-          const float* f1r = p.f1 + (size_t)t * N + dc * 8;
-          const float* f2r = p.f2 + (size_t)t * N + dc * 8;
-          float xh[8], o[8];
-          unpack8(val, xh);
-#pragma unroll
-          for (int i = 0; i < 8; i += 4) {
-            const f32x4 a = *reinterpret_cast<const f32x4*>(f1r + i);
-            const f32x4 c = *reinterpret_cast<const f32x4*>(f2r + i);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[i + e] = xh[i + e] * a[e] + xh[(i + e) ^ 1] * c[e];
+            for (int r = 0; r < 4; ++r) o[r] = qh[r] * a1[r] + qh[r ^ 1] * a2[r];
+            *reinterpret_cast<u32x2*>(outp + hrow * N + n) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
           }
-          val = pack8(o);
         }
-      } else {
-        off = (size_t)m * HN + h * N + dc * 8;
       }
-      st16(base + off, val);
+    } else {
+      const bool is_v = pj == 2;
+#pragma unroll
+      for (int tb = 0; tb < 8; ++tb) {
+        const int m = mrow[tb];
+        if (m >= M) continue;
+        bf16_bits* dst;
+        if (is_v) {
+          const int b = m / T, t = m - b * T;
+          dst = p.v + (((size_t)b * H + h) * T + t) * N;
+        } else {
+          dst = p.sig + (size_t)m * HN + h * N;
+        }
+#pragma unroll
+        for (int j = 0; j < GF; ++j) {
+          const f32x4& a = acc[gi * GF + j][tb];
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = is_v ? a[r] : sigmoidf(a[r]);
+          *reinterpret_cast<u32x2*>(dst + 16 * j + 4 * g) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+        }
+      }
     }
   }
 }
 
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s) {
-  if (N == 64) {
-    const int G = ((p.M + 127) / 128) * p.H;
+  const int G = ((p.M + 255) / 256) * p.H * (4 * N / 256);
+  if (N == 64)
     hipLaunchKernelGGL(qkvg_proj_kernel<64>, dim3(G), dim3(256), 0, s, p);
-  } else {
-    const int G = ((p.M + 63) / 64) * p.H;
+  else
     hipLaunchKernelGGL(qkvg_proj_kernel<128>, dim3(G), dim3(256), 0, s, p);
-  }
   return hipGetLastError();
 }
 
