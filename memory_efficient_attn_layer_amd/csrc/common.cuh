@@ -148,6 +148,11 @@ __device__ __forceinline__ float max_g(float v) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float sigmoidf(float a) { return 1.0f / (1.0f + __expf(-a)); }
+// sigmoid with the hardware exp2 and reciprocal (about 2 ulp in fp32; the
+// result is rounded to bf16).
+__device__ __forceinline__ float fast_sigmoid(float a) {
+  return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-a * kLog2e));
+}
 
 // Row-major bf16 tiles in LDS are stored as 16-byte chunks; chunk c of row r
 // sits at chunk slot c ^ swz(r) of that row. For rows of 8 chunks (128 B)

@@ -21,19 +21,19 @@ constexpr int kSlabK = 64;  // k elements per slab row
 
 __device__ __forceinline__ int slab_swz(int row) { return (row >> 1) & 7; }
 
-// Issues the loads of an R-row slab (R a multiple of 32, shared by the 4
-// waves of the workgroup). rowptr(r, u) returns the global address of element
-// k0 of operand row r; it must be a valid address for every r < R (callers
-// clamp rows past the end of the matrix). u is the unrolled load index: row r
-// lies in [32u, 32u + 32), which lets a caller pick a source matrix per
-// 32-row group at compile time.
-template <int R, class RowPtr>
-__device__ __forceinline__ void slab_issue(bf16_bits* lds, RowPtr rowptr) {
-  static_assert(R % 32 == 0, "slab rows");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Issues the loads of an R-row slab, shared by the NW waves of the
+// workgroup (R a multiple of 8 NW). rowptr(r, u) returns the global address of
+// element k0 of operand row r; it must be a valid address for every r < R
+// (callers clamp rows past the end of the matrix). u is the unrolled load
+// index: row r lies in [8 NW u, 8 NW (u + 1)), which lets a caller pick a
+// source matrix per row group at compile time.
+template <int R, int NW, class RowPtr>
+__device__ __forceinline__ void slab_issue(bf16_bits* lds, int wave, RowPtr rowptr) {
+  static_assert(R % (8 * NW) == 0, "slab rows");
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int u = 0; u < R / 32; ++u) {
-    const int blk = u * 4 + wave;
+  for (int u = 0; u < R / (8 * NW); ++u) {
+    const int blk = u * NW + wave;
     const int row = blk * 8 + (lane >> 3);
     const int chunk = (lane & 7) ^ slab_swz(row);
     g2lds16(rowptr(row, u) + chunk * 8, lds + blk * 512);
