@@ -74,6 +74,15 @@ __device__ __forceinline__ void g2lds16(const void* gsrc, bf16_bits* lds_wave_ba
   const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)((lds_void*)lds_wave_base));
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gsrc), "s"(lds) : "memory");
 }
+// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit
+// per-lane byte offset (saddr form), into the LDS byte address lds (also
+// wave-uniform). Saves the per-lane 64-bit address arithmetic.
+__device__ __forceinline__ void g2lds16_s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)((lds_void*)p); }
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left open), as a builtin so the
 // compiler's own wait tracking also sees every earlier vector load retired.
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }

@@ -21,22 +21,23 @@ constexpr int kSlabK = 64;  // k elements per slab row
 
 __device__ __forceinline__ int slab_swz(int row) { return (row >> 1) & 7; }
 
-// Issues the loads of an R-row slab, shared by the NW waves of the
-// workgroup (R a multiple of 8 NW). rowptr(r, u) returns the global address of
-// element k0 of operand row r; it must be a valid address for every r < R
-// (callers clamp rows past the end of the matrix). u is the unrolled load
-// index: row r lies in [8 NW u, 8 NW (u + 1)), which lets a caller pick a
-// source matrix per row group at compile time.
-template <int R, int NW, class RowPtr>
-__device__ __forceinline__ void slab_issue(bf16_bits* lds, int wave, RowPtr rowptr) {
+// Issues the loads of an R-row slab into LDS byte address lds, shared by the
+// NW waves of the workgroup (R a multiple of 8 NW). Rows come in groups of
+// 8 NW: group u starts at the wave-uniform address base(u) (element k0 of its
+// first row) and its row i (0 <= i < 8 NW) is read from row row_of(u, i) >= 0
+// of that base, rows being stride elements apart. Callers clamp rows past the
+// end of their matrix inside row_of.
+template <int R, int NW, class Base, class RowOf>
+__device__ __forceinline__ void slab_issue(uint32_t lds, int wave, int stride, Base base, RowOf row_of) {
   static_assert(R % (8 * NW) == 0, "slab rows");
   const int lane = threadIdx.x & 63;
+  const int i = wave * 8 + (lane >> 3);
 #pragma unroll
   for (int u = 0; u < R / (8 * NW); ++u) {
-    const int blk = u * NW + wave;
-    const int row = blk * 8 + (lane >> 3);
+    const int row = u * 8 * NW + i;
     const int chunk = (lane & 7) ^ slab_swz(row);
-    g2lds16(rowptr(row, u) + chunk * 8, lds + blk * 512);
+    const uint32_t voff = (uint32_t)(row_of(u, i) * stride + chunk * 8) * 2u;
+    g2lds16_s(base(u), voff, lds + (uint32_t)(u * NW + wave) * 1024u);
   }
 }
 
