@@ -16,18 +16,10 @@ using mea::bf16_bits;
 constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// Number of token slices the weight-gradient reduction is split into.
-inline int dw_splits(int64_t M) {
-  int64_t s = (M + 8191) / 8192;
-  if (s < 1) s = 1;
-  if (s > 16) s = 16;
-  return (int)s;
-}
-
 // Byte offsets of every transient inside the workspace.
 struct Layout {
   size_t q, k, v, sig, o;                    // forward
-  size_t dO, daq, dak, dav, dag;             // backward
+  size_t dO, da;                             // backward; da = [da_q|da_k|da_v|da_g] (M, 4HN)
   size_t rx, rq, rk, delta, woT, wcatT, part;
   size_t total;
 };
@@ -46,17 +38,14 @@ Layout make_layout(const mea_desc& d, int pass) {
     L.o = take(act);
   } else {
     L.dO = take(act);
-    L.daq = take(act);
-    L.dak = take(act);
-    L.dav = take(act);
-    L.dag = take(act);
+    L.da = take(4 * M * HN * 2);
     L.rx = take(M * 4);
     L.rq = take(stat);
     L.rk = take(stat);
     L.delta = take(stat);
     L.woT = take(HN * C * 2);
     L.wcatT = take(C * 4 * HN * 2);
-    L.part = take((size_t)dw_splits((int64_t)M) * (4 * HN * C + C * HN) * 4);
+    L.part = take((size_t)mea::dw_splits((int)M, (int)C, (int)HN) * (4 * HN * C + C * HN) * 4);
   }
   L.total = off;
   return L;
@@ -270,10 +259,11 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   bf16_bits* v = at<bf16_bits>(ws, L.v);
   bf16_bits* sig = at<bf16_bits>(ws, L.sig);
   bf16_bits* dO = at<bf16_bits>(ws, L.dO);
-  bf16_bits* daq = at<bf16_bits>(ws, L.daq);
-  bf16_bits* dak = at<bf16_bits>(ws, L.dak);
-  bf16_bits* dav = at<bf16_bits>(ws, L.dav);
-  bf16_bits* dag = at<bf16_bits>(ws, L.dag);
+  bf16_bits* da = at<bf16_bits>(ws, L.da);  // row stride 4 HN
+  bf16_bits* daq = da;
+  bf16_bits* dak = da + HN;
+  bf16_bits* dav = da + 2 * HN;
+  bf16_bits* dag = da + 3 * HN;
   float* rx = at<float>(ws, L.rx);
   float* rq = at<float>(ws, L.rq);
   float* rk = at<float>(ws, L.rk);
@@ -312,6 +302,7 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   dz.C = C;
   dz.H = H;
   dz.N = N;
+  dz.ld_da = 4 * HN;
   MEA_TRY(timed(K_DZ_GATE_BWD, s, [&] { return mea::launch_dz_gate_bwd(dz, s); }));
 
   mea::AttnBwdParams ab;
@@ -334,25 +325,22 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   ab.B = (int)d->B;
   ab.H = H;
   ab.T = T;
+  ab.ld_da = 4 * HN;
   ab.scale = (float)(1.0 / sqrt((double)N));
   ab.sl2e = (float)(1.0 / sqrt((double)N) * 1.4426950408889634);
   MEA_TRY(timed(K_ATTN_BWD_DQ, s, [&] { return mea::launch_attn_bwd_dq(ab, N, s); }));
   MEA_TRY(timed(K_ATTN_BWD_DKDV, s, [&] { return mea::launch_attn_bwd_dkdv(ab, N, s); }));
 
   mea::DwParams dw;
-  dw.daq = daq;
-  dw.dak = dak;
-  dw.dav = dav;
-  dw.dag = dag;
+  dw.da = da;
   dw.x = static_cast<const bf16_bits*>(x);
   dw.dy = static_cast<const bf16_bits*>(dy);
-  dw.o = static_cast<const bf16_bits*>(o_save);
-  dw.sig = sig;
+  dw.z = sig;  // the dZ kernel replaced sigmoid(a_g) by z = O * sigmoid(a_g)
   dw.part = part;
   dw.M = M;
   dw.C = C;
   dw.HN = HN;
-  dw.splits = dw_splits(M);
+  dw.splits = mea::dw_splits(M, C, HN);
   MEA_TRY(timed(K_DW_PARTIAL, s, [&] { return mea::launch_dw_partial(dw, s); }));
   mea::DwReduceParams dr;
   dr.part = part;
@@ -367,10 +355,7 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   MEA_TRY(timed(K_DW_REDUCE, s, [&] { return mea::launch_dw_reduce(dr, s); }));
 
   mea::DxParams dxp;
-  dxp.daq = daq;
-  dxp.dak = dak;
-  dxp.dav = dav;
-  dxp.dag = dag;
+  dxp.da = da;
   dxp.wcatT = wcatT;
   dxp.x = static_cast<const bf16_bits*>(x);
   dxp.rx = rx;

@@ -32,7 +32,7 @@ namespace mea {
 // for sequence positions t0 .. t0+31 of head (b, h).
 //   rotary != 0 : head RMSNorm + rotary backward of q or k (xrot = q or k).
 //   rotary == 0 : plain copy (v).
-// Output row t goes to out[(b*T + t)*HN + h*N ...], scaled by rx[b*T + t].
+// Output row t goes to out[(b*T + t)*ld_da + h*N ...], scaled by rx[b*T + t].
 template <int N>
 __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, const AttnBwdParams& p,
                                              int b, int h, bool rotary, const bf16_bits* xrot,
@@ -40,7 +40,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
   constexpr int CPR = N / 8, RPP = 64 / CPR;
   const int lane = threadIdx.x & 63;
   const int T = p.T, H = p.H;
-  const size_t HN = (size_t)H * N;
+  const size_t ld = (size_t)p.ld_da;
   const size_t bh = (size_t)b * H + h;
 #pragma unroll 1
   for (int pass = 0; pass < 32 / RPP; ++pass) {
@@ -102,7 +102,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 #pragma unroll
       for (int i = 0; i < 8; ++i) res[i] = rxv * dv[i];
     }
-    if (valid) st16(out + ((size_t)b * T + t) * HN + (size_t)h * N + dc * 8, pack8(res));
+    if (valid) st16(out + ((size_t)b * T + t) * ld + (size_t)h * N + dc * 8, pack8(res));
   }
 }
 

@@ -118,13 +118,14 @@ __global__ __launch_bounds__(256) void dz_gate_bwd_kernel(DzParams p) {
       unpack8(ld16(p.sig + off), sg);
       unpack8(ld16(p.o + off), ov);
       const float rxv = p.rx[mc];
-      float dov[8], dag[8], dl = 0.f;
+      float dov[8], dag[8], zv[8], dl = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         // delta uses the bf16-rounded dO the attention backward consumes, so
         // dP - delta cancels exactly where it should (a single key, T = 1).
         dov[i] = bf2f(f2bf(dz[i] * sg[i]));
         dag[i] = rxv * dz[i] * ov[i] * sg[i] * (1.0f - sg[i]);
+        zv[i] = ov[i] * sg[i];
         dl += dov[i] * ov[i];
       }
       dl += xor1(dl);
@@ -136,7 +137,8 @@ __global__ __launch_bounds__(256) void dz_gate_bwd_kernel(DzParams p) {
         const int b = mc / T, t = mc - b * T;
         const size_t hrow = ((size_t)b * H + hh) * T + t;
         st16(p.dO + hrow * N + n, pack8(dov));
-        st16(p.dag + off, pack8(dag));
+        st16(p.dag + (size_t)mc * p.ld_da + jc, pack8(dag));
+        st16(p.sig + off, pack8(zv));  // sigmoid(a_g) is dead from here on
         if (n == 0) p.delta[hrow] = dl;
       }
     }
@@ -173,9 +175,7 @@ __global__ __launch_bounds__(256) void dx_kernel(DxParams p) {
   auto load_a = [&](int row, int k0, int kc, int) -> u32x4 {
     const int m = m0 + row;
     if (m >= M) return u32x4{0u, 0u, 0u, 0u};
-    const int pj = k0 / HN, col = k0 - pj * HN + kc * 8;
-    const bf16_bits* src = pj == 0 ? p.daq : pj == 1 ? p.dak : pj == 2 ? p.dav : p.dag;
-    return ld16(src + (size_t)m * HN + col);
+    return ld16(p.da + (size_t)m * K4 + k0 + kc * 8);
   };
   auto load_b = [&](int row, int k0, int kc, int) -> u32x4 {
     return ld16(p.wcatT + (size_t)row * K4 + k0 + kc * 8);
@@ -245,89 +245,128 @@ hipError_t launch_dx(const DxParams& p, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Weight gradients: D(i, j) = sum_m A(m, i) B(m, j) over a token slice.
-// Both operands are token-major, so each 32-token slab is written into LDS
-// transposed (pairs of tokens packed into 32-bit words) and then read as
-// ordinary k-contiguous MFMA fragments.
+// Weight gradients D(i, j) = sum_m A(m, i) B(m, j) over a token range:
+//   problem 0: A = da (M, 4HN), B = x (M, C)   -> dWcat (4HN, C)
+//   problem 1: A = dy (M, C),   B = z (M, HN)  -> dWo   (C, HN)
+// Both operands are token-major. Slabs of 32 tokens x 256 features land in
+// LDS row-major (direct global->LDS loads, 3 stages); the MFMA operands,
+// which run along tokens, are read with the transposing ds_read_b64_tr_b16.
+// Tile 256 x 256, eight waves of 64 (i) x 128 (j). The token range is split
+// so that all tiles x splits fill the CUs once; fp32 partials are summed by
+// dw_reduce in a fixed order.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void dw_partial_kernel(DwParams p) {
-  constexpr int BT = 128, P = kLdsPitch;  // tile 128 x 128, 32 tokens per step
-  __shared__ __attribute__((aligned(16))) bf16_bits At[BT * P];
-  __shared__ __attribute__((aligned(16))) bf16_bits Bt[BT * P];
-  const int M = p.M, C = p.C, HN = p.HN, K4 = 4 * HN;
-  const int ti0 = K4 / BT, tj0 = C / BT;                  // dWcat tiles
-  const int tj1 = (HN + BT - 1) / BT;                     // dWo tiles
-  const int tile = blockIdx.x, z = blockIdx.y;
-  const bool prob1 = tile >= ti0 * tj0;
-  const int lt = prob1 ? tile - ti0 * tj0 : tile;
-  const int ntj = prob1 ? tj1 : tj0;
-  const int i0 = (lt / ntj) * BT, j0 = (lt % ntj) * BT;
-  const int I = prob1 ? C : K4, J = prob1 ? HN : C;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+namespace {
+
+constexpr int kDwBK = 32;     // tokens per slab
+constexpr int kDwTile = 256;  // output tile edge
+constexpr int kDwSlab = kDwBK * kDwTile;  // elements per operand slab
+
+// Chunk c (16 bytes) of slab row r sits at slot c ^ dw_swz(r). The eight
+// rows that one half-wave reads in a transposing read (rows 0-3 and 8-11 of
+// an 8-row group pair) then cover eight distinct 32-byte bank segments.
+__device__ __forceinline__ int dw_swz(int r) { return ((r & 3) | ((r >> 1) & 4)) << 1; }
+
+// Loads one 32 x 256 slab: rows m0 .. m0+31 (clamped to M-1), columns
+// c0 .. c0+255 (clamped to ncol-8) of a row-major (M, ld) matrix.
+__device__ __forceinline__ void dw_issue(uint32_t lds, int wave, const bf16_bits* src, int ld, int m0, int M,
+                                         int c0, int ncol) {
+  const int lane = threadIdx.x & 63;
+  const int mb = min(m0, M - 1);
+  const bf16_bits* base = src + (size_t)mb * ld + c0;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int ins = u * 8 + wave;         // 16 instructions of 2 rows each
+    const int row = 2 * ins + (lane >> 5);
+    const int chunk = (lane & 31) ^ dw_swz(row);
+    const int r = min(m0 + row, M - 1) - mb;
+    const int col = min(8 * chunk, ncol - c0 - 8);
+    g2lds16_s(base, (uint32_t)(r * ld + col) * 2u, lds + (uint32_t)ins * 1024u);
+  }
+}
+
+// MFMA operand of feature block f (16 features) from a slab: lane (g, c16)
+// gets feature 16 f + c16 of tokens 8g .. 8g+7.
+__device__ __forceinline__ bf16x8 dw_frag(const bf16_bits* slab, int f, int lane) {
   const int c16 = lane & 15, g = lane >> 4;
+  const int r0 = 8 * g + (c16 >> 2);
+  const int col = 16 * f + 4 * (c16 & 3);
+  const int ch = col >> 3, within = col & 7;
+  const bf16_bits* p0 = slab + r0 * kDwTile + ((ch ^ dw_swz(r0)) << 3) + within;
+  const bf16_bits* p1 = slab + (r0 + 4) * kDwTile + ((ch ^ dw_swz(r0 + 4)) << 3) + within;
+  return frag_from2(lds_read_tr4(p0), lds_read_tr4(p1));
+}
 
-  const int chunk = ((M + (int)gridDim.y - 1) / (int)gridDim.y + 31) / 32 * 32;
+}  // namespace
+
+__global__ __launch_bounds__(512, 1) void dw_partial_kernel(DwParams p) {
+  constexpr int STAGES = 3;
+  __shared__ __attribute__((aligned(16))) bf16_bits smem[STAGES * 2 * kDwSlab];
+  const int M = p.M, C = p.C, HN = p.HN, K4 = 4 * HN;
+  const int t0 = (K4 / kDwTile) * (C / kDwTile);           // problem-0 tiles
+  const int t1 = (C / kDwTile) * ((HN + kDwTile - 1) / kDwTile);
+  const int ntile = t0 + t1;
+  // Consecutive logical ids (same token split, neighbouring tiles) share an
+  // XCD, so the operand rows of a split are fetched into one L2.
+  const int L = xcd_remap(blockIdx.x, ntile * p.splits);
+  const int z = L / ntile, tile = L - z * ntile;
+  const bool prob1 = tile >= t0;
+  const int lt = prob1 ? tile - t0 : tile;
+  const int ntj = prob1 ? (HN + kDwTile - 1) / kDwTile : C / kDwTile;
+  const int i0 = (lt / ntj) * kDwTile, j0 = (lt % ntj) * kDwTile;
+  const int I = prob1 ? C : K4, J = prob1 ? HN : C;
+  const bf16_bits* asrc = prob1 ? p.dy : p.da;
+  const bf16_bits* bsrc = prob1 ? p.z : p.x;
+  const int lda = prob1 ? C : K4, ldb = prob1 ? HN : C;
+
+  const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wi = wave & 3, wj = wave >> 2;
+
+  const int chunk = ((M + p.splits - 1) / p.splits + kDwBK - 1) / kDwBK * kDwBK;
   const int mbeg = z * chunk, mend = min(M, mbeg + chunk);
+  const int ns = mbeg < mend ? (mend - mbeg + kDwBK - 1) / kDwBK : 0;
 
-  // One row pair x 8 columns per thread per operand.
-  const int rp = tid >> 4, cc = tid & 15;
-  auto ld_a = [&](int m) -> u32x4 {
-    const int i = i0 + cc * 8;
-    if (m >= mend || i >= I) return u32x4{0u, 0u, 0u, 0u};
-    if (prob1) return ld16(p.dy + (size_t)m * C + i);
-    const int pj = i / HN, col = i - pj * HN;
-    const bf16_bits* src = pj == 0 ? p.daq : pj == 1 ? p.dak : pj == 2 ? p.dav : p.dag;
-    return ld16(src + (size_t)m * HN + col);
-  };
-  auto ld_b = [&](int m) -> u32x4 {
-    const int j = j0 + cc * 8;
-    if (m >= mend || j >= J) return u32x4{0u, 0u, 0u, 0u};
-    if (!prob1) return ld16(p.x + (size_t)m * C + j);
-    float o[8], s[8];
-    unpack8(ld16(p.o + (size_t)m * HN + j), o);
-    unpack8(ld16(p.sig + (size_t)m * HN + j), s);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] *= s[e];
-    return pack8(o);
-  };
-  auto put_t = [&](bf16_bits* dstT, const u32x4& r0, const u32x4& r1) {
-    uint32_t* dst = reinterpret_cast<uint32_t*>(dstT + (cc * 8) * P + 2 * rp);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      dst[(2 * e) * P / 2] = (r0[e] & 0xffffu) | (r1[e] << 16);
-      dst[(2 * e + 1) * P / 2] = (r0[e] >> 16) | (r1[e] & 0xffff0000u);
-    }
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int s) {
+    const int st = s % STAGES;
+    const uint32_t lds = lds0 + (uint32_t)(st * 2 * kDwSlab) * 2u;
+    const int m0 = mbeg + s * kDwBK;
+    dw_issue(lds, wave, asrc, lda, m0, M, i0, I);
+    dw_issue(lds + kDwSlab * 2, wave, bsrc, ldb, m0, M, j0, J);
   };
 
-  f32x4 acc[4][4];
+  f32x4 acc[4][8];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[a][c] = zero4();
+    for (int b = 0; b < 8; ++b) acc[a][b] = zero4();
 
-  u32x4 a0, a1, b0, b1;
-  auto fetch = [&](int m) {
-    a0 = ld_a(m + 2 * rp);
-    a1 = ld_a(m + 2 * rp + 1);
-    b0 = ld_b(m + 2 * rp);
-    b1 = ld_b(m + 2 * rp + 1);
-  };
-  if (mbeg < mend) fetch(mbeg);
-  for (int m = mbeg; m < mend; m += 32) {
-    put_t(At, a0, a1);
-    put_t(Bt, b0, b1);
+  if (ns > 0) issue(0);
+  if (ns > 1) issue(1);
+  for (int s = 0; s < ns; ++s) {
+    // Slab s has landed once at most the next slab's 4 loads are pending.
+    if (s + 1 < ns)
+      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+    else
+      wait_vmcnt0();
     __syncthreads();
-    if (m + 32 < mend) fetch(m + 32);
-    bf16x8 af[4], bfr[4];
+    bf16_bits* As = smem + (s % STAGES) * 2 * kDwSlab;
+    const int valid = mend - (mbeg + s * kDwBK);
+    if (valid < kDwBK) {
+      // Last slab of the matrix: token rows past the end contribute zero.
+      for (int e = tid; e < (kDwBK - valid) * kDwTile; e += 512) As[valid * kDwTile + e] = 0;
+      __syncthreads();
+    }
+    if (s + 2 < ns) issue(s + 2);
+    bf16x8 af[4], bfr[8];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) af[a] = as_frag(*reinterpret_cast<const u32x4*>(At + (wm * 64 + a * 16 + c16) * P + 8 * g));
+    for (int a = 0; a < 4; ++a) af[a] = dw_frag(As, wi * 4 + a, lane);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) bfr[c] = as_frag(*reinterpret_cast<const u32x4*>(Bt + (wn * 64 + c * 16 + c16) * P + 8 * g));
+    for (int b = 0; b < 8; ++b) bfr[b] = dw_frag(As + kDwSlab, wj * 8 + b, lane);
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[a][c] = mfma(af[a], bfr[c], acc[a][c]);
-    __syncthreads();
+      for (int b = 0; b < 8; ++b) acc[a][b] = mfma(af[a], bfr[b], acc[a][b]);
   }
 
   const size_t per_split = (size_t)K4 * C + (size_t)C * HN;
@@ -335,20 +374,35 @@ __global__ __launch_bounds__(256) void dw_partial_kernel(DwParams p) {
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int j = j0 + wn * 64 + c * 16 + c16;
+    for (int b = 0; b < 8; ++b) {
+      const int j = j0 + wj * 128 + b * 16 + c16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = i0 + wm * 64 + a * 16 + 4 * g + r;
-        if (i < I && j < J) out[(size_t)i * J + j] = acc[a][c][r];
+        const int i = i0 + wi * 64 + a * 16 + 4 * g + r;
+        if (i < I && j < J) out[(size_t)i * J + j] = acc[a][b][r];
       }
     }
 }
 
+int dw_splits(int M, int C, int HN) {
+  const int tiles = (4 * HN / kDwTile) * (C / kDwTile) + (C / kDwTile) * ((HN + kDwTile - 1) / kDwTile);
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus = n;
+  }
+  int s = cus / tiles;
+  const int max_s = (M + kDwBK - 1) / kDwBK;
+  if (s > max_s) s = max_s;
+  return s < 1 ? 1 : s;
+}
+
 hipError_t launch_dw_partial(const DwParams& p, hipStream_t s) {
-  const int K4 = 4 * p.HN;
-  const int tiles = (K4 / 128) * (p.C / 128) + (p.C / 128) * ((p.HN + 127) / 128);
-  hipLaunchKernelGGL(dw_partial_kernel, dim3(tiles, p.splits), dim3(256), 0, s, p);
+  const int tiles = (4 * p.HN / kDwTile) * (p.C / kDwTile) + (p.C / kDwTile) * ((p.HN + kDwTile - 1) / kDwTile);
+  hipLaunchKernelGGL(dw_partial_kernel, dim3(tiles * p.splits), dim3(512), 0, s, p);
   return hipGetLastError();
 }
 

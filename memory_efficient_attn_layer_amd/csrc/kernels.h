@@ -41,9 +41,10 @@ struct AttnBwdParams {
   const float *f1, *f2;                     // (T_max, N)
   const float* rx;                          // (M)
   const float *rq, *rk;                     // (B, H, T)
-  bf16_bits *daq, *dak, *dav;               // (M, H*N), rows scaled by rx
+  bf16_bits *daq, *dak, *dav;               // (M, H*N) column blocks of the (M, 4*H*N)
+                                            // gradient, row stride ld_da; rows scaled by rx
   float *df1, *df2;                         // (T, N) accumulators or null
-  int B, H, T;
+  int B, H, T, ld_da;
   float scale, sl2e;
 };
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s);
@@ -60,24 +61,27 @@ hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s);
 
 // dZ = dy Wo, then the gate backward:
 //   dO = dZ * sig            -> (B, H, T, N)
-//   da_g = rx * dZ * O * sig * (1 - sig)   -> (M, HN)
+//   da_g = rx * dZ * O * sig * (1 - sig)   -> (M, HN), row stride ld_da
 //   delta = rowsum_N(dO * O) -> (B, H, T)
+//   z = O * sig              -> (M, HN), written over sig (the output
+//                               projection's input, for dWo)
 struct DzParams {
   const bf16_bits* dy;                      // (M, C)
   const bf16_bits* woT;                     // (HN, C)
-  const bf16_bits *o, *sig;                 // (M, HN)
+  const bf16_bits* o;                       // (M, HN)
+  bf16_bits* sig;                           // (M, HN): sigmoid(a_g) in, z out
   const float* rx;                          // (M)
   bf16_bits* dO;                            // (B, H, T, N)
-  bf16_bits* dag;                           // (M, HN)
+  bf16_bits* dag;                           // (M, HN) block of the (M, 4HN) gradient
   float* delta;                             // (B, H, T)
-  int M, T, C, H, N;
+  int M, T, C, H, N, ld_da;
 };
 hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s);
 
 // acc = [daq|dak|dav|dag] Wcat  (rows pre-scaled by rx), then the input
 // RMSNorm backward: dx = acc - x * rx^2 * (acc . x) / C.
 struct DxParams {
-  const bf16_bits *daq, *dak, *dav, *dag;   // (M, HN)
+  const bf16_bits* da;                      // (M, 4*HN) = [da_q | da_k | da_v | da_g]
   const bf16_bits* wcatT;                   // (C, 4*HN)
   const bf16_bits* x;                       // (M, C)
   const float* rx;                          // (M)
@@ -87,16 +91,19 @@ struct DxParams {
 hipError_t launch_dx(const DxParams& p, hipStream_t s);
 
 // Weight gradients, split over tokens into fp32 partial sums:
-//   dWcat = [daq|dak|dav|dag]^T x        (4*HN, C)
-//   dWo   = dy^T (o * sig)               (C, HN)
+//   dWcat = da^T x        (4*HN, C)   da = [da_q | da_k | da_v | da_g]
+//   dWo   = dy^T z        (C, HN)     z = O * sig
 struct DwParams {
-  const bf16_bits *daq, *dak, *dav, *dag;   // (M, HN)
+  const bf16_bits* da;                      // (M, 4*HN)
   const bf16_bits* x;                       // (M, C)
   const bf16_bits* dy;                      // (M, C)
-  const bf16_bits *o, *sig;                 // (M, HN)
+  const bf16_bits* z;                       // (M, HN)
   float* part;                              // (splits, 4*HN*C + C*HN)
   int M, C, HN, splits;
 };
+// Token splits of the weight-gradient reduction for a shape (one workgroup
+// per CU over all output tiles); the workspace holds that many partials.
+int dw_splits(int M, int C, int HN);
 hipError_t launch_dw_partial(const DwParams& p, hipStream_t s);
 // Sums the partials and writes the five bf16 weight gradients.
 struct DwReduceParams {
