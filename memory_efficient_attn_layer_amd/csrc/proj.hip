@@ -12,10 +12,13 @@
 // is an in-lane sum plus two lane exchanges, both members of every rotary
 // pair (n, n^1) sit in one lane, and results leave as 8-byte stores.
 //
-// Tile: 256 features x 256 tokens, k-slabs of 64 double-buffered in LDS and
-// filled by direct global->LDS loads (one barrier per slab). Eight waves, two
-// per SIMD, each owning one projection's features of its tokens: 64 features
-// x 128 tokens for N = 64, 128 x 64 for N = 128 (32 accumulators of 16x16).
+// Tile: 256 features x 128 tokens. k-slabs of 32 stream through a 3-stage
+// LDS ring filled by direct global->LDS loads, two slabs ahead, continuously
+// across the tiles a workgroup walks (one barrier per slab). Four waves of
+// 128 features x 64 tokens (32 accumulators of 16x16): for N = 64 a wave owns
+// two projections of its tokens, (q, k) or (v, g), so the rotary table rows
+// of its tokens are fetched once for both q and k. Two workgroups share a CU,
+// so one's epilogue overlaps the other's products.
 //
 // The input RMSNorm is never materialised: diag(1/rms(x)) commutes with the
 // GEMM, so the row scale multiplies the fp32 accumulator. The row sums of
@@ -28,34 +31,40 @@
 
 namespace mea {
 
-// Tile coordinates of logical tile L: token tile (head-minor order, so the
-// tiles of one token tile are consecutive and share their x rows in L2).
+// Tile coordinates of logical tile L (head-minor order, so the tiles of one
+// token tile are consecutive and share their x rows in L2).
 struct ProjTile {
   int m0, h, f0;
 };
 
+constexpr int kProjBT = 128;  // tokens per tile
+constexpr int kProjBF = 256;  // stacked-weight rows per tile
+constexpr int kProjBK = 32;   // k per slab
+constexpr int kProjStages = 3;
+
 template <int N>
 __device__ __forceinline__ ProjTile proj_tile(int L, int H) {
-  constexpr int NFT = 4 * N / 256;
+  constexpr int NFT = 4 * N / kProjBF;
   const int tt = L / (H * NFT), rem = L - tt * (H * NFT);
-  return ProjTile{tt * 256, rem / NFT, (rem % NFT) * 256};
+  return ProjTile{tt * kProjBT, rem / NFT, (rem % NFT) * kProjBF};
 }
 
-// Persistent: one workgroup per CU walks tiles; the first k-slab of its next
-// tile is loaded while the current tile's epilogue runs. Workgroup w runs on
-// XCD w % 8 and takes tiles from a contiguous range owned by that XCD, so the
-// workgroups of one XCD work on neighbouring tiles at the same time.
+// Persistent: workgroups walk tiles; workgroup w runs on XCD w % 8 and takes
+// tiles from a contiguous range owned by that XCD, so the workgroups of one
+// XCD work on neighbouring tiles at the same time.
 template <int N>
-__global__ __launch_bounds__(512, 1) void qkvg_proj_kernel(ProjParams p) {
-  constexpr int BT = 256;              // tokens per tile
-  constexpr int BF = 256;              // stacked-weight rows per tile
-  constexpr int STAGE = (BF + BT) * kSlabK;
-  constexpr int WF = BF / N;           // waves along features (one projection each)
-  constexpr int WT = 8 / WF;           // waves along tokens
-  constexpr int FB = N / 16;           // 16-feature blocks per wave
-  constexpr int TB = BT / WT / 16;     // 16-token blocks per wave
+__global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
+  constexpr int BT = kProjBT, BF = kProjBF, BK = kProjBK, NS = kProjStages;
+  constexpr int STAGE = (BF + BT) * BK;
+  constexpr int WF = 2, WT = 2;        // waves along features x tokens
+  constexpr int FB = 8;                // 16-feature blocks per wave (128 features)
+  constexpr int TB = BT / WT / 16;     // 16-token blocks per wave (4)
   constexpr int GB = TB / WF;          // Gram blocks per wave
-  __shared__ __attribute__((aligned(16))) bf16_bits smem[2 * STAGE];
+  constexpr int NPW = 128 / N;         // projections per wave
+  constexpr int GF = N / 16;           // feature blocks per projection
+  constexpr int NSEG = BF / N;         // projections per stacked-weight slab
+  constexpr int LOADS = (BF + BT) * BK / 8 / 64 / 4;  // load instructions per wave per slab
+  __shared__ __attribute__((aligned(16))) bf16_bits smem[NS * STAGE];
   __shared__ float ssq_s[BT];
 
   // Locals, not captures of the argument block: a lambda holding &p would
@@ -67,30 +76,36 @@ __global__ __launch_bounds__(512, 1) void qkvg_proj_kernel(ProjParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wf = wave % WF, wt = wave / WF;
 
-  // This workgroup's tiles: start + j, start + j + nj, ... (< start + cnt).
+  // This workgroup's tiles: start + j0 + i * nj for i < ntl.
   const int ntiles = ((M + BT - 1) / BT) * H * (4 * N / BF);
   const int G = gridDim.x, xcd = blockIdx.x & 7, j0 = blockIdx.x >> 3;
   const int nj = (G - xcd + 7) >> 3;
   const int q8 = ntiles >> 3, r8 = ntiles & 7;
   const int start = xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8;
   const int cnt = xcd < r8 ? q8 + 1 : q8;
+  const int ntl = j0 < cnt ? (cnt - j0 + nj - 1) / nj : 0;
+  const int nk = C / BK;
+  const int nslab = ntl * nk;  // slabs this workgroup streams, over all its tiles
 
   const uint32_t lds0 = lds_addr(smem);
-  auto issue = [&](const ProjTile& tl, int ks, int st) {
-    const uint32_t lds = lds0 + (uint32_t)(st * STAGE) * 2u;
-    const int k0 = ks * kSlabK;
-    const bf16_bits* wseg[WF];
-    if (WF == 4) {
+  // Issues slab q of the stream: tile q / nk, k-slab q % nk, into stage q % NS.
+  auto issue = [&](int q) {
+    const int ti = q / nk, ks = q - ti * nk;
+    const ProjTile tl = proj_tile<N>(start + j0 + ti * nj, H);
+    const uint32_t lds = lds0 + (uint32_t)((q % NS) * STAGE) * 2u;
+    const int k0 = ks * BK;
+    const bf16_bits* wseg[NSEG];
+    if (NSEG == 4) {
       wseg[0] = wq;
-      wseg[WF > 1 ? 1 : 0] = wk;
-      wseg[WF > 2 ? 2 : 0] = wv;
-      wseg[WF > 3 ? 3 : 0] = wg;
+      wseg[NSEG > 1 ? 1 : 0] = wk;
+      wseg[NSEG > 2 ? 2 : 0] = wv;
+      wseg[NSEG > 3 ? 3 : 0] = wg;
     } else {
       wseg[0] = tl.f0 == 0 ? wq : wv;
-      wseg[WF > 1 ? 1 : 0] = tl.f0 == 0 ? wk : wg;
+      wseg[NSEG > 1 ? 1 : 0] = tl.f0 == 0 ? wk : wg;
     }
-    // Stacked-weight rows: group u (64 rows) lies inside one projection.
-    slab_issue<BF, 8>(
+    // Stacked-weight rows: each 64-row load group lies inside one projection.
+    slab_issue<BF, 4, BK>(
         lds, wave, C,
         [&](int u) {
           const int seg = (64 * u) / N;  // compile-time after unrolling
@@ -98,8 +113,8 @@ __global__ __launch_bounds__(512, 1) void qkvg_proj_kernel(ProjParams p) {
         },
         [](int, int i) { return i; });
     // x rows, clamped to the last token.
-    slab_issue<BT, 8>(
-        lds + BF * kSlabK * 2, wave, C,
+    slab_issue<BT, 4, BK>(
+        lds + BF * BK * 2, wave, C,
         [&](int u) { return xg + (size_t)min(tl.m0 + 64 * u, M - 1) * C + k0; },
         [&](int u, int i) { return min(tl.m0 + 64 * u + i, M - 1) - min(tl.m0 + 64 * u, M - 1); });
   };
@@ -107,17 +122,33 @@ __global__ __launch_bounds__(512, 1) void qkvg_proj_kernel(ProjParams p) {
   f32x4 acc[FB][TB];
   f32x4 gram[GB];  // Gram blocks of token blocks GB*wf .. GB*wf+GB-1
 
-  // One k-slab from LDS stage st: 2 x (FB*TB + GB) MFMAs.
-  auto compute = [&](int st) {
-    const bf16_bits* As = smem + st * STAGE;
-    const bf16_bits* Bs = As + BF * kSlabK;
+  if (nslab > 0) issue(0);
+  if (nslab > 1) issue(1);
+  for (int ti = 0; ti < ntl; ++ti) {
+    const ProjTile tl = proj_tile<N>(start + j0 + ti * nj, H);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int fb = 0; fb < FB; ++fb)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = zero4();
+#pragma unroll
+    for (int i = 0; i < GB; ++i) gram[i] = zero4();
+
+    for (int ks = 0; ks < nk; ++ks) {
+      const int q = ti * nk + ks;
+      // Slab q has landed once at most the next slab's loads are pending.
+      if (q + 1 < nslab)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);  // vmcnt(LOADS)
+      else
+        wait_vmcnt0();
+      __syncthreads();
+      if (q + 2 < nslab) issue(q + 2);
+      const bf16_bits* As = smem + (q % NS) * STAGE;
+      const bf16_bits* Bs = As + BF * BK;
       bf16x8 af[FB], bfr[TB];
 #pragma unroll
-      for (int fb = 0; fb < FB; ++fb) af[fb] = as_frag(slab_read(As, wf * N + fb * 16 + c16, 4 * kk + g));
+      for (int fb = 0; fb < FB; ++fb) af[fb] = as_frag(slab_read<BK>(As, wf * 128 + fb * 16 + c16, g));
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) bfr[tb] = as_frag(slab_read(Bs, wt * (TB * 16) + tb * 16 + c16, 4 * kk + g));
+      for (int tb = 0; tb < TB; ++tb) bfr[tb] = as_frag(slab_read<BK>(Bs, wt * (TB * 16) + tb * 16 + c16, g));
 #pragma unroll
       for (int fb = 0; fb < FB; ++fb)
 #pragma unroll
@@ -130,35 +161,6 @@ __global__ __launch_bounds__(512, 1) void qkvg_proj_kernel(ProjParams p) {
         gram[i] = mfma(xb, xb, gram[i]);
       }
     }
-  };
-
-  const int nk = C / kSlabK;
-  if (j0 < cnt) issue(proj_tile<N>(start + j0, H), 0, 0);
-  for (int jt = j0; jt < cnt; jt += nj) {
-    const ProjTile tl = proj_tile<N>(start + jt, H);
-    const bool has_next = jt + nj < cnt;
-    const ProjTile nx = proj_tile<N>(start + (has_next ? jt + nj : jt), H);
-
-#pragma unroll
-    for (int fb = 0; fb < FB; ++fb)
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = zero4();
-#pragma unroll
-    for (int i = 0; i < GB; ++i) gram[i] = zero4();
-
-    // Double-buffered main loop: one barrier per slab; the next slab's loads
-    // (after the last slab: the next tile's first) are in flight while this
-    // one is multiplied. Slab ks lives in stage ks & 1 (nk is even).
-    for (int ks = 0; ks + 1 < nk; ++ks) {
-      wait_vmcnt0();
-      __syncthreads();
-      issue(tl, ks + 1, (ks + 1) & 1);
-      compute(ks & 1);
-    }
-    wait_vmcnt0();
-    __syncthreads();
-    if (has_next) issue(nx, 0, 0);
-    compute(1);
 
     // Diagonal of each Gram block: token c16 of the block sits in lane
     // (g = c16 / 4, c16), register c16 % 4.
@@ -173,13 +175,14 @@ __global__ __launch_bounds__(512, 1) void qkvg_proj_kernel(ProjParams p) {
     __syncthreads();
 
     // Row coordinates. A tile inside one sequence (the usual case: T a
-    // multiple of 256) needs no per-row division or bounds checks.
+    // multiple of 128) needs no per-row division or bounds checks.
     const int m0 = tl.m0, h = tl.h;
     const float inv_c = 1.0f / (float)C, inv_n = 1.0f / (float)N, eps = p.eps;
     const int b0 = m0 / T, t0 = m0 - b0 * T;
     const bool whole = m0 + BT <= M && t0 + BT <= T;
     int trow[TB], brow[TB];
     bool ok[TB];
+    float rx[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
       const int tlr = wt * (TB * 16) + tb * 16 + c16, m = m0 + tlr;
@@ -192,63 +195,106 @@ __global__ __launch_bounds__(512, 1) void qkvg_proj_kernel(ProjParams p) {
         trow[tb] = m - brow[tb] * T;
         ok[tb] = m < M;
       }
-      const float rx = rsqrtf(ssq_s[tlr] * inv_c + eps);
-      if (p.rx != nullptr && h == 0 && tl.f0 == 0 && wf == 0 && g == 0 && ok[tb]) p.rx[m] = rx;
-#pragma unroll
-      for (int fb = 0; fb < FB; ++fb) acc[fb][tb] *= rx;
+      rx[tb] = rsqrtf(ssq_s[tlr] * inv_c + eps);
+      if (p.rx != nullptr && h == 0 && tl.f0 == 0 && wf == 0 && g == 0 && ok[tb]) p.rx[m] = rx[tb];
     }
 
-    const int pj = (tl.f0 + wf * N) / N;  // this wave's projection (wave-uniform)
-    if (pj < 2) {
-      // Head RMSNorm over N (fast_triton_attn.py:102-106), then the rotary
-      // from the bf16-rounded normalised values, the reference's rounding
-      // point (:103, :140): out[n] = qh[n] f1[t,n] + qh[n^1] f2[t,n].
-      float* rstat = pj == 0 ? p.rq : p.rk;
-      bf16_bits* outp = pj == 0 ? p.q : p.k;
+    // Output staging: the stage of the tile's last slab is free until the
+    // next tile's third slab is issued (after that tile's first barrier).
+    // Each wave owns a 16-token x (NPW * N) block of it, rows of N + 8
+    // elements, filled with 8-byte writes from the accumulator layout and
+    // drained as 16-byte row chunks, so every store covers whole rows.
+    constexpr int SP = N + 8;
+    bf16_bits* stg = smem + ((ti * nk + nk - 1) % NS) * STAGE + wave * (NPW * 16 * SP);
+    const int pj0 = (tl.f0 + wf * 128) / N;  // first projection of this wave (wave-uniform)
+    constexpr int CPR = N / 8;               // 16-byte chunks per output row
+    // Drains the staged block of projection gi for token block tb into
+    // dstp + b * bstride + t * tstride.
+    auto drain = [&](int gi, int tb, bf16_bits* dstp, size_t bstride, size_t tstride) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        float s = 0.f;
-#pragma unroll
-        for (int fb = 0; fb < FB; ++fb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) s += acc[fb][tb][r] * acc[fb][tb][r];
-        s += shfl_xor(s, 16);
-        s += shfl_xor(s, 32);
-        const float rr = rsqrtf(s * inv_n + eps);
-        if (ok[tb]) {
-          const int t = trow[tb];
-          const size_t hrow = ((size_t)brow[tb] * H + h) * T + t;
-          if (rstat != nullptr && g == 0) rstat[hrow] = rr;
-          const float* f1r = p.f1 + (size_t)t * N;
-          const float* f2r = p.f2 + (size_t)t * N;
-#pragma unroll
-          for (int fb = 0; fb < FB; ++fb) {
-            const int n = 16 * fb + 4 * g;
-            const f32x4 a1 = *reinterpret_cast<const f32x4*>(f1r + n);
-            const f32x4 a2 = *reinterpret_cast<const f32x4*>(f2r + n);
-            float qh[4], o[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) qh[r] = bf2f(f2bf(acc[fb][tb][r] * rr));
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[r] = qh[r] * a1[r] + qh[r ^ 1] * a2[r];
-            *reinterpret_cast<u32x2*>(outp + hrow * N + n) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
-          }
+      for (int it = 0; it < 16 * CPR / 64; ++it) {
+        const int id = lane + 64 * it, row = id / CPR, ch = id % CPR;
+        const int tl_row = wt * (TB * 16) + tb * 16 + row;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + (gi * 16 + row) * SP + ch * 8);
+        if (whole || m0 + tl_row < M) {
+          const int m = m0 + tl_row;
+          const int bb = whole ? b0 : m / T, tt = whole ? t0 + tl_row : m - (m / T) * T;
+          st16(dstp + (size_t)bb * bstride + (size_t)tt * tstride + ch * 8, val);
         }
       }
-    } else {
-      const bool is_v = pj == 2;
+    };
+    if (pj0 < 2) {
+      // Head RMSNorm over N (fast_triton_attn.py:102-106) of a = rx * acc:
+      // 1/rms(a) = rsqrt(rx^2 mean(acc^2) + eps), one scale rx / rms(a) per
+      // row. The rotary (:132-141) then acts on the fp32 normalised values:
+      // out[n] = qh[n] f1[t,n] + qh[n^1] f2[t,n].
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) {
-        if (!ok[tb]) continue;
-        bf16_bits* dst = is_v ? p.v + (((size_t)brow[tb] * H + h) * T + trow[tb]) * N
-                              : p.sig + ((size_t)brow[tb] * T + trow[tb]) * HN + h * N;
+        float sc[NPW], rr[NPW];
 #pragma unroll
-        for (int fb = 0; fb < FB; ++fb) {
-          const f32x4& a = acc[fb][tb];
-          float o[4];
+        for (int gi = 0; gi < NPW; ++gi) {
+          float s = 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = is_v ? a[r] : fast_sigmoid(a[r]);
-          *reinterpret_cast<u32x2*>(dst + 16 * fb + 4 * g) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+          for (int j = 0; j < GF; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s += acc[gi * GF + j][tb][r] * acc[gi * GF + j][tb][r];
+          s += shfl_xor(s, 16);
+          s += shfl_xor(s, 32);
+          rr[gi] = rsqrtf(rx[tb] * rx[tb] * s * inv_n + eps);
+          sc[gi] = rx[tb] * rr[gi];
+        }
+        const int t = ok[tb] ? trow[tb] : 0;
+        if (ok[tb] && g == 0) {
+          const size_t hrow = ((size_t)brow[tb] * H + h) * T + t;
+#pragma unroll
+          for (int gi = 0; gi < NPW; ++gi) {
+            float* rstat = pj0 + gi == 0 ? p.rq : p.rk;
+            if (rstat != nullptr) rstat[hrow] = rr[gi];
+          }
+        }
+        const float* f1r = p.f1 + (size_t)t * N;
+        const float* f2r = p.f2 + (size_t)t * N;
+#pragma unroll
+        for (int j = 0; j < GF; ++j) {
+          const int n = 16 * j + 4 * g;
+          const f32x4 a1 = *reinterpret_cast<const f32x4*>(f1r + n);
+          const f32x4 a2 = *reinterpret_cast<const f32x4*>(f2r + n);
+#pragma unroll
+          for (int gi = 0; gi < NPW; ++gi) {
+            const f32x4& a = acc[gi * GF + j][tb];
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] = (a[r] * a1[r] + a[r ^ 1] * a2[r]) * sc[gi];
+            *reinterpret_cast<u32x2*>(stg + (gi * 16 + c16) * SP + n) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+          }
+        }
+#pragma unroll
+        for (int gi = 0; gi < NPW; ++gi)
+          drain(gi, tb, (pj0 + gi == 0 ? p.q : p.k) + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
+      }
+    } else {
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+        for (int gi = 0; gi < NPW; ++gi) {
+          const bool is_v = pj0 + gi == 2;
+#pragma unroll
+          for (int j = 0; j < GF; ++j) {
+            const f32x4& a = acc[gi * GF + j][tb];
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] = is_v ? a[r] * rx[tb] : fast_sigmoid(a[r] * rx[tb]);
+            *reinterpret_cast<u32x2*>(stg + (gi * 16 + c16) * SP + 16 * j + 4 * g) =
+                u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+          }
+        }
+#pragma unroll
+        for (int gi = 0; gi < NPW; ++gi) {
+          if (pj0 + gi == 2)
+            drain(gi, tb, p.v + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
+          else
+            drain(gi, tb, p.sig + (size_t)h * N, (size_t)T * HN, (size_t)HN);
         }
       }
     }
@@ -256,7 +302,7 @@ __global__ __launch_bounds__(512, 1) void qkvg_proj_kernel(ProjParams p) {
 }
 
 // Workgroups per device for the persistent kernels: one per CU.
-int persistent_grid(int tiles) {
+int persistent_grid(int tiles, int per_cu) {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -265,15 +311,15 @@ int persistent_grid(int tiles) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     cus[dev] = n;
   }
-  return tiles < cus[dev] ? tiles : cus[dev];
+  return tiles < per_cu * cus[dev] ? tiles : per_cu * cus[dev];
 }
 
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s) {
-  const int G = persistent_grid(((p.M + 255) / 256) * p.H * (4 * N / 256));
+  const int G = persistent_grid(((p.M + kProjBT - 1) / kProjBT) * p.H * (4 * N / kProjBF), 2);
   if (N == 64)
-    hipLaunchKernelGGL(qkvg_proj_kernel<64>, dim3(G), dim3(512), 0, s, p);
+    hipLaunchKernelGGL(qkvg_proj_kernel<64>, dim3(G), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(qkvg_proj_kernel<128>, dim3(G), dim3(512), 0, s, p);
+    hipLaunchKernelGGL(qkvg_proj_kernel<128>, dim3(G), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

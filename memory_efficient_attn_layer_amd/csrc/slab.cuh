@@ -1,49 +1,56 @@
 // LDS k-slabs for the GEMM-shaped kernels (gfx950).
 //
-// A slab holds R operand rows x 64 bf16 of the reduction dimension k
-// (128 bytes = 8 chunks of 16 bytes per row). Chunk c of row r sits at chunk
-// slot c ^ ((r >> 1) & 7): two rows fill one 256-byte LDS bank line, so the
-// 16 rows that one 16-lane group reads at one chunk index land in 16 distinct
-// 16-byte bank groups.
+// A slab holds R operand rows x KS bf16 of the reduction dimension k, KS = 64
+// (8 chunks of 16 bytes per row) or 32 (4 chunks). Chunk c of row r sits at
+// chunk slot c ^ slab_swz<KS>(r): with 64-element rows two rows fill one
+// 256-byte LDS bank line (swizzle (r >> 1) & 7), with 32-element rows four do
+// (swizzle (r >> 2) & 3); either way the 16 rows that one 16-lane group reads
+// at one chunk index land in 16 distinct 16-byte bank groups.
 //
 // Slabs are filled straight from global memory with global_load_lds_dwordx4:
-// one wave instruction writes 1 KB (8 rows) of LDS, lane L filling slot L & 7
-// of row L >> 3; the swizzle is applied by choosing which global chunk each
-// lane fetches, so every 8 lanes still read one contiguous 128-byte row
-// segment.
+// one wave instruction writes 1 KB of LDS (64 / CH rows), lane L filling slot
+// L % CH of row L / CH; the swizzle is applied by choosing which global chunk
+// each lane fetches, so every CH lanes still read one contiguous row segment.
 #pragma once
 
 #include "common.cuh"
 
 namespace mea {
 
-constexpr int kSlabK = 64;  // k elements per slab row
+constexpr int kSlabK = 64;  // k elements per row of a 64-wide slab
 
-__device__ __forceinline__ int slab_swz(int row) { return (row >> 1) & 7; }
+template <int KS>
+__device__ __forceinline__ int slab_swz(int row) {
+  static_assert(KS == 64 || KS == 32, "slab width");
+  return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
 
 // Issues the loads of an R-row slab into LDS byte address lds, shared by the
-// NW waves of the workgroup (R a multiple of 8 NW). Rows come in groups of
-// 8 NW: group u starts at the wave-uniform address base(u) (element k0 of its
-// first row) and its row i (0 <= i < 8 NW) is read from row row_of(u, i) >= 0
-// of that base, rows being stride elements apart. Callers clamp rows past the
-// end of their matrix inside row_of.
-template <int R, int NW, class Base, class RowOf>
+// NW waves of the workgroup. Rows come in groups of G = NW * 64 / CH (the
+// rows one round of load instructions covers): group u starts at the
+// wave-uniform address base(u) (element k0 of its first row) and its row i
+// (0 <= i < G) is read from row row_of(u, i) >= 0 of that base, rows being
+// stride elements apart. Callers clamp rows past the end of their matrix
+// inside row_of.
+template <int R, int NW, int KS, class Base, class RowOf>
 __device__ __forceinline__ void slab_issue(uint32_t lds, int wave, int stride, Base base, RowOf row_of) {
-  static_assert(R % (8 * NW) == 0, "slab rows");
+  constexpr int CH = KS / 8, RPI = 64 / CH, G = NW * RPI;
+  static_assert(R % G == 0, "slab rows");
   const int lane = threadIdx.x & 63;
-  const int i = wave * 8 + (lane >> 3);
+  const int i = wave * RPI + lane / CH;
 #pragma unroll
-  for (int u = 0; u < R / (8 * NW); ++u) {
-    const int row = u * 8 * NW + i;
-    const int chunk = (lane & 7) ^ slab_swz(row);
+  for (int u = 0; u < R / G; ++u) {
+    const int row = u * G + i;
+    const int chunk = (lane % CH) ^ slab_swz<KS>(row);
     const uint32_t voff = (uint32_t)(row_of(u, i) * stride + chunk * 8) * 2u;
     g2lds16_s(base(u), voff, lds + (uint32_t)(u * NW + wave) * 1024u);
   }
 }
 
-// 16-byte read of chunk `chunk` (0..7) of slab row `row`.
+// 16-byte read of chunk `chunk` of slab row `row`.
+template <int KS>
 __device__ __forceinline__ u32x4 slab_read(const bf16_bits* lds, int row, int chunk) {
-  return *reinterpret_cast<const u32x4*>(lds + row * kSlabK + ((chunk ^ slab_swz(row)) << 3));
+  return *reinterpret_cast<const u32x4*>(lds + row * KS + ((chunk ^ slab_swz<KS>(row)) << 3));
 }
 
 // Sum of squares of 8 bf16 values (exact fp32 products, fp32 accumulation).
