@@ -18,7 +18,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 // Byte offsets of every transient inside the workspace.
 struct Layout {
-  size_t q, k, v, sig, o;                    // forward
+  size_t q, k, v, sig, o, qkn;               // forward
   size_t dO, da;                             // backward; da = [da_q|da_k|da_v|da_g] (M, 4HN)
   size_t rx, rq, rk, delta, woT, wcatT, part;
   size_t total;
@@ -36,6 +36,7 @@ Layout make_layout(const mea_desc& d, int pass) {
   L.sig = take(act);
   if (pass == MEA_PASS_FWD) {
     L.o = take(act);
+    L.qkn = take(2 * sizeof(float));
   } else {
     L.dO = take(act);
     L.da = take(4 * M * HN * 2);
@@ -144,9 +145,17 @@ size_t mea_workspace_bytes(const mea_desc* d, int pass) {
   return make_layout(*d, pass).total;
 }
 
-int mea_qkvg_proj(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv,
-                  const void* wg, const float* f1, const float* f2, void* q, void* k, void* v, void* sig,
-                  float* rx, float* rq, float* rk, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// log2(e)/sqrt(N): the block stores q in these units, so the attention's
+// logits come out of the MFMA ready for exp2.
+float q_log2_scale(int64_t N) { return (float)(1.4426950408889634 / sqrt((double)N)); }
+
+int proj_impl(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+              const float* f1, const float* f2, void* q, void* k, void* v, void* sig, float* rx, float* rq,
+              float* rk, float qscale, float* qk_norm2, void* stream) {
   int rc = validate(d, MEA_PASS_FWD);
   if (rc != MEA_OK) return rc;
   rc = check_ptrs({x, wq, wk, wv, wg, f1, f2, q, k, v, sig});
@@ -166,6 +175,8 @@ int mea_qkvg_proj(const mea_desc* d, const void* x, const void* wq, const void* 
   p.rx = rx;
   p.rq = rq;
   p.rk = rk;
+  p.qk_norm2 = qk_norm2;
+  p.qscale = qscale;
   p.M = (int)(d->B * d->T);
   p.T = (int)d->T;
   p.C = (int)d->C;
@@ -176,8 +187,22 @@ int mea_qkvg_proj(const mea_desc* d, const void* x, const void* wq, const void* 
   return MEA_OK;
 }
 
-int mea_attn_fwd(const mea_desc* d, const void* q, const void* k, const void* v, void* o, float* lse,
-                 void* stream) {
+}  // namespace
+
+extern "C" {
+
+int mea_qkvg_proj(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv,
+                  const void* wg, const float* f1, const float* f2, void* q, void* k, void* v, void* sig,
+                  float* rx, float* rq, float* rk, void* stream) {
+  return proj_impl(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, 1.0f, nullptr, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int attn_fwd_impl(const mea_desc* d, const void* q, const void* k, const void* v, void* o, float* lse, float sl2e,
+                  const float* qk_norm2, void* stream) {
   int rc = validate(d, MEA_PASS_FWD);
   if (rc != MEA_OK) return rc;
   rc = check_ptrs({q, k, v, o});
@@ -191,10 +216,20 @@ int mea_attn_fwd(const mea_desc* d, const void* q, const void* k, const void* v,
   p.B = (int)d->B;
   p.H = (int)d->H;
   p.T = (int)d->T;
-  p.sl2e = (float)(1.0 / sqrt((double)d->N) * 1.4426950408889634);
+  p.sl2e = sl2e;
+  p.qk_norm2 = qk_norm2;
   hipStream_t s = static_cast<hipStream_t>(stream);
   MEA_TRY(timed(K_ATTN_FWD, s, [&] { return mea::launch_attn_fwd(p, (int)d->N, s); }));
   return MEA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mea_attn_fwd(const mea_desc* d, const void* q, const void* k, const void* v, void* o, float* lse,
+                 void* stream) {
+  return attn_fwd_impl(d, q, k, v, o, lse, q_log2_scale(d->N), nullptr, stream);
 }
 
 int mea_gate_oproj(const mea_desc* d, const void* o, const void* sig, const void* wo, void* y, void* stream) {
@@ -231,9 +266,15 @@ int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk, co
   void* v = at<void>(ws, L.v);
   void* sig = at<void>(ws, L.sig);
   void* o = o_save != nullptr ? o_save : at<void>(ws, L.o);
-  rc = mea_qkvg_proj(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, nullptr, nullptr, nullptr, stream);
+  // q is stored in log2 units; the projection records the largest q and k
+  // row norms so the attention can take its fixed-offset softmax.
+  float* qkn = at<float>(ws, L.qkn);
+  MEA_TRY(timed(K_ZERO, static_cast<hipStream_t>(stream),
+                [&] { return mea::launch_zero_f32(qkn, 2, static_cast<hipStream_t>(stream)); }));
+  const float qs = q_log2_scale(d->N);
+  rc = proj_impl(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, nullptr, nullptr, nullptr, qs, qkn, stream);
   if (rc != MEA_OK) return rc;
-  rc = mea_attn_fwd(d, q, k, v, o, lse_save, stream);
+  rc = attn_fwd_impl(d, q, k, v, o, lse_save, 1.0f, qkn, stream);
   if (rc != MEA_OK) return rc;
   return mea_gate_oproj(d, o, sig, wo, y, stream);
 }
@@ -285,7 +326,8 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   }
 
   // Recompute q, k, v, sigmoid(g) and the three RMS statistics.
-  rc = mea_qkvg_proj(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, stream);
+  const float qs = q_log2_scale(N);
+  rc = proj_impl(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, qs, nullptr, stream);
   if (rc != MEA_OK) return rc;
 
   mea::DzParams dz;
@@ -327,7 +369,8 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   ab.T = T;
   ab.ld_da = 4 * HN;
   ab.scale = (float)(1.0 / sqrt((double)N));
-  ab.sl2e = (float)(1.0 / sqrt((double)N) * 1.4426950408889634);
+  ab.sl2e = 1.0f;  // q was stored in log2 units by the recompute above
+  ab.qscale = qs;
   MEA_TRY(timed(K_ATTN_BWD_DQ, s, [&] { return mea::launch_attn_bwd_dq(ab, N, s); }));
   MEA_TRY(timed(K_ATTN_BWD_DKDV, s, [&] { return mea::launch_attn_bwd_dkdv(ab, N, s); }));
 

@@ -30,12 +30,13 @@ namespace mea {
 
 // Row-wise tail for one wave: 32 staged rows of fp32 gradient (pitch FP)
 // for sequence positions t0 .. t0+31 of head (b, h).
-//   rotary != 0 : head RMSNorm + rotary backward of q or k (xrot = q or k).
+//   rotary != 0 : head RMSNorm + rotary backward of q or k (xrot = q or k
+//                 as stored, xrot * xscale the rotated rows themselves).
 //   rotary == 0 : plain copy (v).
 // Output row t goes to out[(b*T + t)*ld_da + h*N ...], scaled by rx[b*T + t].
 template <int N>
 __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, const AttnBwdParams& p,
-                                             int b, int h, bool rotary, const bf16_bits* xrot,
+                                             int b, int h, bool rotary, const bf16_bits* xrot, float xscale,
                                              const float* rstat, bf16_bits* out) {
   constexpr int CPR = N / 8, RPP = 64 / CPR;
   const int lane = threadIdx.x & 63;
@@ -60,6 +61,8 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
     if (rotary) {
       float xv[8], a1[8], a2[8];
       unpack8(ld16(xrot + (bh * T + tc) * N + dc * 8), xv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[i] *= xscale;
       const float* f1r = p.f1 + (size_t)tc * N + dc * 8;
       const float* f2r = p.f2 + (size_t)tc * N + dc * 8;
 #pragma unroll
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdParams p) {
     for (int db = 0; db < DB; ++db)
       *reinterpret_cast<f32x4*>(stg + (qb * 16 + c16) * FP + db * 16 + 4 * g) = dq[db][qb] * p.scale;
   __syncthreads();
-  head_row_bwd<N>(stg, FP, qw0, p, b, h, true, p.q, p.rq, p.daq);
+  head_row_bwd<N>(stg, FP, qw0, p, b, h, true, p.q, 1.0f / p.qscale, p.rq, p.daq);
 }
 
 // ---------------------------------------------------------------------------
@@ -464,17 +467,17 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
         *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v;
       }
     __syncthreads();
-    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, b, hd, false, nullptr, nullptr, p.dav);
+    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, b, hd, false, nullptr, 1.0f, nullptr, p.dav);
     __syncthreads();
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const f32x4 v = {dk[kb][db][4 * r4], dk[kb][db][4 * r4 + 1], dk[kb][db][4 * r4 + 2], dk[kb][db][4 * r4 + 3]};
-        *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v * p.scale;
+        *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v * (p.scale / p.qscale);
       }
     __syncthreads();
-    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, b, hd, true, p.k, p.rk, p.dak);
+    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, b, hd, true, p.k, 1.0f, p.rk, p.dak);
     __syncthreads();
   }
 }

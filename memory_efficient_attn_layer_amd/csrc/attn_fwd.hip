@@ -19,11 +19,22 @@
 //                   transposing ds_read_b64_tr_b16, B = P^T straight from
 //                   the S^T accumulator registers (keys in the order the
 //                   accumulator holds them, matched by the V^T rows read).
-// The running maximum is only raised when a new score exceeds it by more
-// than 2^8 (in exp2 units); probabilities stay below 2^8, and the costly
-// rescale of the output accumulator is skipped on almost every step.
+//
+// Two softmax forms:
+//  - fixed offset: q and k come out of a per-head RMSNorm, so every logit is
+//    bounded by |q| |k|. When the caller passes the row-norm bounds, q is
+//    stored in log2 units (sl2e == 1) and the bound is at most kFixedBound,
+//    P = exp2(q.k) needs no running maximum at all: P lies in
+//    [2^-60, 2^60], far inside the fp32/bf16 range, and O = sum P v / sum P
+//    is the same quotient the running-maximum form computes. Per score that
+//    leaves one exp2, one add and half a convert.
+//  - online: the running maximum is only raised when a new score exceeds it
+//    by more than 2^8 (in exp2 units), so the costly rescale of the output
+//    accumulator is skipped on almost every step.
 // The output is written straight into the (B, T, H*N) layout the output
 // projection reads (the reference's gate_repack layout, :171-176).
+#include <type_traits>
+
 #include "common.cuh"
 #include "kernels.h"
 
@@ -52,13 +63,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   const int lid = xcd_remap(blockIdx.x, BH * nqb);
   const int bh = lid / nqb, qi = nqb - 1 - lid % nqb;
   const int b = bh / p.H, hd = bh % p.H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, h = lane >> 5;
   const int q0w = qi * BQ + wave * QW;
   const int kv_end = min(T, qi * BQ + BQ);
   const size_t head_off = (size_t)bh * T * N;
   const bf16_bits* kg = p.k + head_off;
   const bf16_bits* vg = p.v + head_off;
+
+  bool fixed = false;
+  if (p.qk_norm2 != nullptr && p.sl2e == 1.0f) {
+    const float bound = sqrtf(p.qk_norm2[0] * p.qk_norm2[1]) * 1.01f;
+    fixed = bound <= kFixedBound;
+  }
 
   // Q^T fragments (B operand): lane holds query q0w + 32qb + c, d = 16ks + 8h.
   bf16x8 qf[QB][KS];
@@ -85,7 +103,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   f32x16 o[QB][DB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    m_i[qb] = -INFINITY;
+    m_i[qb] = fixed ? 0.f : -INFINITY;
     l_i[qb] = 0.f;
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[qb][db] = zero16();
@@ -96,42 +114,45 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   const int tr_row = 4 * h + (i16 >> 2);             // + 16*kstep + 8*t (+ 32*st)
   const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);  // + 32*db
 
-  const int nkv = (kv_end + BKV - 1) / BKV;
-  issue_tile(0, 0);
-  wait_vmcnt0();  // also retires the Q fragment loads
-  __syncthreads();
-  for (int j = 0; j < nkv; ++j) {
-    if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
-    const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
-    const bf16_bits* vs_t = ks_t + TILE;
+  // One 32-key step of every query block of this wave. FIXED: exp2 of the
+  // raw logit; otherwise the online form. MASK: the step touches the causal
+  // diagonal or the end of the sequence.
+  auto step = [&](const bf16_bits* ks_t, const bf16_bits* vs_t, int st, int kb0, auto fixed_tag, auto mask_tag) {
+    constexpr bool FIXED = decltype(fixed_tag)::value;
+    constexpr bool MASK = decltype(mask_tag)::value;
+    bf16x8 kf[KS];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const int kb0 = j * BKV + st * 32;
-      if (kb0 > q0w + QW - 1) continue;  // every key of the step is in this wave's future
-      bf16x8 kf[KS];
+    for (int ks = 0; ks < KS; ++ks)
+      kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + swz_off<CH>(st * 32 + c, 16 * ks + 8 * h)));
+    bf16x8 pf[QB][2];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + swz_off<CH>(st * 32 + c, 16 * ks + 8 * h)));
-      bf16x8 pf[QB][2];
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qb0 = q0w + 32 * qb;
+      if (MASK && kb0 > qb0 + 31) {
+        // The whole step is in this query block's future: contributes nothing.
+        pf[qb][0] = pf[qb][1] = as_frag(u32x4{0u, 0u, 0u, 0u});
+        continue;
+      }
+      f32x16 s = zero16();
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const int qb0 = q0w + 32 * qb;
-        if (kb0 > qb0 + 31) {
-          // The whole step is masked for this query block: contributes nothing.
-          pf[qb][0] = pf[qb][1] = as_frag(u32x4{0u, 0u, 0u, 0u});
-          continue;
-        }
-        f32x16 s = zero16();
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) s = mfma32(kf[ks], qf[qb][ks], s);
+      for (int ks = 0; ks < KS; ++ks) s = mfma32(kf[ks], qf[qb][ks], s);
+      if (MASK) {
         const int qq = qb0 + c;
-        if (kb0 + 31 > qb0 || kb0 + 32 > T) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (key > qq || key >= T) s[i] = -INFINITY;
-          }
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (key > qq || key >= T) s[i] = -INFINITY;
         }
+      }
+      float ls = 0.f;
+      if (FIXED) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = fast_exp2(s[i]);
+          s[i] = e;
+          ls += e;
+        }
+      } else {
         float mx = s[0];
 #pragma unroll
         for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
@@ -147,41 +168,65 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
           m_i[qb] = mn;
         }
         const float nm = -m_i[qb];
-        float ls = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const float e = fast_exp2(__builtin_fmaf(s[i], p.sl2e, nm));
           s[i] = e;
           ls += e;
         }
-        l_i[qb] += ls;
-#pragma unroll
-        for (int kst = 0; kst < 2; ++kst) {
-          u32x4 w;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
-          pf[qb][kst] = as_frag(w);
-        }
       }
-      // O^T += V^T P^T, two 16-key MFMA steps.
+      l_i[qb] += ls;
 #pragma unroll
       for (int kst = 0; kst < 2; ++kst) {
+        u32x4 w;
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const int r = st * 32 + 16 * kst + tr_row, col = 32 * db + tr_col;
-          const bf16x8 vf = frag_from2(lds_read_tr4(vs_t + swz_off<CH>(r, col)),
-                                       lds_read_tr4(vs_t + swz_off<CH>(r + 8, col)));
+        for (int e = 0; e < 4; ++e) w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
+        pf[qb][kst] = as_frag(w);
+      }
+    }
+    // O^T += V^T P^T, two 16-key MFMA steps.
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) {
-            if (kb0 > q0w + 32 * qb + 31) continue;
-            o[qb][db] = mfma32(vf, pf[qb][kst], o[qb][db]);
-          }
+    for (int kst = 0; kst < 2; ++kst) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int r = st * 32 + 16 * kst + tr_row, col = 32 * db + tr_col;
+        const bf16x8 vf = frag_from2(lds_read_tr4(vs_t + swz_off<CH>(r, col)),
+                                     lds_read_tr4(vs_t + swz_off<CH>(r + 8, col)));
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          if (MASK && kb0 > q0w + 32 * qb + 31) continue;
+          o[qb][db] = mfma32(vf, pf[qb][kst], o[qb][db]);
         }
       }
     }
-    wait_vmcnt0();
+  };
+
+  auto main_loop = [&](auto fixed_tag) {
+    const int nkv = (kv_end + BKV - 1) / BKV;
+    issue_tile(0, 0);
+    wait_vmcnt0();  // also retires the Q fragment loads
     __syncthreads();
-  }
+    for (int j = 0; j < nkv; ++j) {
+      if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
+      const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
+      const bf16_bits* vs_t = ks_t + TILE;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int kb0 = j * BKV + st * 32;
+        if (kb0 > q0w + QW - 1) continue;  // every key of the step is in this wave's future
+        if (kb0 + 31 < q0w && kb0 + 32 <= T)
+          step(ks_t, vs_t, st, kb0, fixed_tag, std::false_type{});
+        else
+          step(ks_t, vs_t, st, kb0, fixed_tag, std::true_type{});
+      }
+      wait_vmcnt0();
+      __syncthreads();
+    }
+  };
+  if (fixed)
+    main_loop(std::true_type{});
+  else
+    main_loop(std::false_type{});
 
   // Normalise, write lse and stage O^T (lane = query) as rows for 16-byte stores.
   bf16_bits* stg = smem + wave * QW * OP;

@@ -18,8 +18,12 @@ struct ProjParams {
   bf16_bits* sig;                           // (M, H*N)
   float* rx;                                // (M) or null
   float *rq, *rk;                           // (B, H, T) or null
+  // Largest squared norms of the stored q and k rows (2 floats, zeroed
+  // beforehand, raised with atomic max) or null.
+  float* qk_norm2;
   int M, T, C, H;
   float eps;
+  float qscale;                             // the stored q rows are q * qscale
 };
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s);
 
@@ -27,10 +31,14 @@ hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s);
 struct AttnFwdParams {
   const bf16_bits *q, *k, *v;               // (B, H, T, N)
   bf16_bits* o;                             // (B, T, H*N)
-  float* lse;                               // (B, H, T) or null
+  float* lse;                               // (B, H, T) natural log, or null
+  // Squared-norm bounds of the q and k rows (see ProjParams) or null. When
+  // given and sl2e * |q| |k| <= kFixedBound, the softmax runs without a max.
+  const float* qk_norm2;
   int B, H, T;
-  float sl2e;                               // softmax scale * log2(e)
+  float sl2e;                               // multiplies q.k into log2 units
 };
+constexpr float kFixedBound = 60.0f;
 hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s);
 
 // Causal flash attention backward fused with the q/k RMSNorm + rotary
@@ -45,7 +53,9 @@ struct AttnBwdParams {
                                             // gradient, row stride ld_da; rows scaled by rx
   float *df1, *df2;                         // (T, N) accumulators or null
   int B, H, T, ld_da;
-  float scale, sl2e;
+  float scale;                              // softmax scale 1/sqrt(N)
+  float sl2e;                               // multiplies stored q . k into log2 units
+  float qscale;                             // stored q = q * qscale
 };
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s);
 hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s);

@@ -228,10 +228,15 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       // Head RMSNorm over N (fast_triton_attn.py:102-106) of a = rx * acc:
       // 1/rms(a) = rsqrt(rx^2 mean(acc^2) + eps), one scale rx / rms(a) per
       // row. The rotary (:132-141) then acts on the fp32 normalised values:
-      // out[n] = qh[n] f1[t,n] + qh[n^1] f2[t,n].
+      // out[n] = qh[n] f1[t,n] + qh[n^1] f2[t,n]; q rows are stored times
+      // qscale. The largest squared row norm of each projection is recorded
+      // for the attention's logit bound.
+      float nmax[NPW];
+#pragma unroll
+      for (int gi = 0; gi < NPW; ++gi) nmax[gi] = 0.f;
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) {
-        float sc[NPW], rr[NPW];
+        float sc[NPW], rr[NPW], nrm[NPW];
 #pragma unroll
         for (int gi = 0; gi < NPW; ++gi) {
           float s = 0.f;
@@ -242,7 +247,8 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
           s += shfl_xor(s, 16);
           s += shfl_xor(s, 32);
           rr[gi] = rsqrtf(rx[tb] * rx[tb] * s * inv_n + eps);
-          sc[gi] = rx[tb] * rr[gi];
+          sc[gi] = rx[tb] * rr[gi] * (pj0 + gi == 0 ? p.qscale : 1.0f);
+          nrm[gi] = 0.f;
         }
         const int t = ok[tb] ? trow[tb] : 0;
         if (ok[tb] && g == 0) {
@@ -265,13 +271,35 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
             const f32x4& a = acc[gi * GF + j][tb];
             float o[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[r] = (a[r] * a1[r] + a[r ^ 1] * a2[r]) * sc[gi];
+            for (int r = 0; r < 4; ++r) {
+              o[r] = (a[r] * a1[r] + a[r ^ 1] * a2[r]) * sc[gi];
+              nrm[gi] += o[r] * o[r];
+            }
             *reinterpret_cast<u32x2*>(stg + (gi * 16 + c16) * SP + n) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
           }
         }
 #pragma unroll
+        for (int gi = 0; gi < NPW; ++gi) {
+          float v = nrm[gi];
+          v += shfl_xor(v, 16);
+          v += shfl_xor(v, 32);
+          nmax[gi] = fmaxf(nmax[gi], v);
+        }
+#pragma unroll
         for (int gi = 0; gi < NPW; ++gi)
           drain(gi, tb, (pj0 + gi == 0 ? p.q : p.k) + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
+      }
+      if (p.qk_norm2 != nullptr) {
+#pragma unroll
+        for (int gi = 0; gi < NPW; ++gi) {
+          float v = nmax[gi];
+          v = fmaxf(v, xor1(v));
+          v = fmaxf(v, xor2(v));
+          v = fmaxf(v, shfl_xor(v, 4));
+          v = fmaxf(v, shfl_xor(v, 8));
+          // Non-negative floats order like their bit patterns.
+          if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(p.qk_norm2) + (pj0 + gi), __float_as_uint(v));
+        }
       }
     } else {
 #pragma unroll

@@ -102,6 +102,19 @@ def test_block_forward_backward(label, w, B):
     check_block(w, B=B)
 
 
+@pytest.mark.parametrize("tscale", [2.0, 2.5], ids=["fixed-offset-wide-range", "online-fallback"])
+def test_block_logit_range(tscale):
+    """Rotary tables scaled by tscale widen the logit range. The block bounds
+    every logit by |q| |k| log2(e)/sqrt(N) (about 11.5 tscale^2 here): 2.0
+    (~46) keeps the fixed-offset softmax with probabilities down to 2^-92 of
+    the largest, 2.5 (~72) exceeds its limit of 60 and takes the online
+    softmax. Both must match the oracle."""
+    inp = make_inputs(W0, B=1)
+    f1 = (inp["f1"].float() * tscale).to(torch.bfloat16)
+    f2 = (inp["f2"].float() * tscale).to(torch.bfloat16)
+    check_block(W0, B=1, f1=f1, f2=f2)
+
+
 def test_block_without_table_grad_matches():
     got, _ = check_block(W0, table_grad=False)
     assert got["df1"] is None and got["df2"] is None
