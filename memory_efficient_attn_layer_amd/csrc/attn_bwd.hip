@@ -14,13 +14,14 @@
 // recompute pass does not have to keep the pre-rotation values.
 //
 // Two kernels (deterministic, no atomics on dQ):
-//   dq kernel   : one workgroup per (b, h, 128 queries), streams key tiles.
-//                 S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - delta),
-//                 dQ^T += K^T dS^T.
-//   dkdv kernel : one workgroup per (b, h, 128 keys), streams query tiles.
-//                 S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
-// Operands that reduce over a sequence index (K^T, Q^T, dO^T) are written
-// into LDS transposed, as 32-bit pairs of adjacent rows.
+//   dq kernel   : one workgroup per (b, h, 4 waves of queries), streams key
+//                 tiles. S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T -
+//                 delta), dQ^T += K^T dS^T.
+//   dkdv kernel : one workgroup per (b, h, 4 waves of keys), streams query
+//                 tiles. S = Q K^T, dP = dO V^T, dV^T += dO^T P,
+//                 dK^T += Q^T dS.
+// Operands that reduce over a sequence index (K^T, Q^T, dO^T) are read from
+// row-major LDS tiles with the transposing ds_read_b64_tr_b16.
 #include <type_traits>
 
 #include "common.cuh"
@@ -111,160 +112,193 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 
 // ---------------------------------------------------------------------------
 // dQ
+//
+// One workgroup = one (batch, head) and BQ = 4*QW queries; wave w owns QW
+// consecutive queries (64 for N = 64, 32 for N = 128) whose q and dO rows
+// stay in registers as the B operands of
+//   S^T = K Q^T   and   dP^T = V dO^T      (A = K, V rows from LDS)
+// on v_mfma_f32_32x32x16_bf16. The query index sits on the lane, so the row
+// statistics lse and delta are per-lane registers and dS^T = P^T (dP^T -
+// delta) is already the B operand (k = key) of
+//   dQ^T += K^T dS^T
+// whose A operand K^T is read from the row-major K tile with the transposing
+// ds_read_b64_tr_b16. Key tiles of 64 stream through LDS (global_load_lds,
+// double-buffered, one barrier per tile); tiles below the workgroup's first
+// query run in a branch-free loop, the diagonal region after it.
 // ---------------------------------------------------------------------------
 template <int N>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdParams p) {
-  constexpr int BQ = 128, BKV = 64, QW = 32;
-  constexpr int KP = N + 8, TP = BKV + 8;
-  constexpr int NS = N / 32, DB = N / 16, FP = N + 4;
-  constexpr int SM_LOOP = (2 * BKV * KP + N * TP) * 2;  // bytes
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
+  constexpr int QW = N == 64 ? 64 : 32;  // queries per wave
+  constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
+  constexpr int BQ = 4 * QW;             // queries per workgroup
+  constexpr int BKV = 64;                // keys per LDS tile
+  constexpr int CH = N / 8, KS = N / 16, DB = N / 32;
+  constexpr int TILE = BKV * N;
+  constexpr int LOADS = TILE / 8 / 256;
+  constexpr int FP = N + 4;  // fp32 staging pitch
+  constexpr int SM_LOOP = 4 * TILE * 2;  // bytes: [stage][K | V]
   constexpr int SM_OUT = 4 * QW * FP * 4;
   constexpr int SMEM = SM_LOOP > SM_OUT ? SM_LOOP : SM_OUT;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
-  bf16_bits* Ks = reinterpret_cast<bf16_bits*>(smem);
-  bf16_bits* Vs = Ks + BKV * KP;
-  bf16_bits* Kt = Vs + BKV * KP;
+  __shared__ __attribute__((aligned(16))) unsigned char smem_raw[SMEM];
+  bf16_bits* smem = reinterpret_cast<bf16_bits*>(smem_raw);
 
-  const int T = p.T, H = p.H, BH = p.B * p.H;
+  const int T = p.T, BH = p.B * p.H;
   const int nqb = (T + BQ - 1) / BQ;
-  const int L = blockIdx.x;
-  const int bh = L % BH, qi = nqb - 1 - L / BH;
-  const int b = bh / H, h = bh % H;
-  const int q0 = qi * BQ;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
-  const int qw0 = q0 + wave * QW;
+  // Each XCD walks whole heads (heaviest query block first), so the K/V
+  // tiles of a head are fetched once into that XCD's L2.
+  const int lid = xcd_remap(blockIdx.x, BH * nqb);
+  const int bh = lid / nqb, qi = nqb - 1 - lid % nqb;
+  const int b = bh / p.H, hd = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, h = lane >> 5;
+  const int q0w = qi * BQ + wave * QW;
+  const int kv_end = min(T, qi * BQ + BQ);
   const size_t head_off = (size_t)bh * T * N;
   const bf16_bits* kg = p.k + head_off;
   const bf16_bits* vg = p.v + head_off;
 
-  bf16x8 qf[2][NS], df[2][NS];
-  float lse2[2], dlt[2];
+  // q^T and dO^T fragments (B operands) and the row statistics of the lane's
+  // query q0w + 32qb + c.
+  bf16x8 qf[QB][KS], df[QB][KS];
+  float lse2[QB], dlt[QB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int t = qw0 + qb * 16 + c16;
-    const bool ok = t < T;
+  for (int qb = 0; qb < QB; ++qb) {
+    const int t = min(q0w + 32 * qb + c, T - 1);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const size_t off = head_off + (size_t)t * N + s * 32 + 8 * g;
-      qf[qb][s] = as_frag(ok ? ld16(p.q + off) : u32x4{0u, 0u, 0u, 0u});
-      df[qb][s] = as_frag(ok ? ld16(p.dO + off) : u32x4{0u, 0u, 0u, 0u});
+    for (int ks = 0; ks < KS; ++ks) {
+      const size_t off = head_off + (size_t)t * N + 16 * ks + 8 * h;
+      qf[qb][ks] = as_frag(ld16(p.q + off));
+      df[qb][ks] = as_frag(ld16(p.dO + off));
     }
-    lse2[qb] = ok ? p.lse[(size_t)bh * T + t] * kLog2e : 0.f;
-    dlt[qb] = ok ? p.delta[(size_t)bh * T + t] : 0.f;
+    lse2[qb] = p.lse[(size_t)bh * T + t] * kLog2e;
+    dlt[qb] = p.delta[(size_t)bh * T + t];
   }
 
-  constexpr int KCH = BKV * N / 8 / 256;          // row chunks per thread
-  constexpr int PCH = (BKV / 2) * (N / 8) / 256;  // row-pair chunks per thread
-  u32x4 rk[KCH], rv[KCH], rp0[PCH], rp1[PCH];
-  auto fetch = [&](int j0) {
+  auto issue_tile = [&](int j0, int stage) {
+    bf16_bits* kt = smem + stage * 2 * TILE;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (N / 8), dc = id % (N / 8);
-      const int t = j0 + row;
-      rk[i] = t < T ? ld16(kg + (size_t)t * N + dc * 8) : u32x4{0u, 0u, 0u, 0u};
-      rv[i] = t < T ? ld16(vg + (size_t)t * N + dc * 8) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < PCH; ++i) {
-      const int id = tid + 256 * i, rp = id / (N / 8), dc = id % (N / 8);
-      const int t = j0 + 2 * rp;
-      rp0[i] = t < T ? ld16(kg + (size_t)t * N + dc * 8) : u32x4{0u, 0u, 0u, 0u};
-      rp1[i] = t + 1 < T ? ld16(kg + (size_t)(t + 1) * N + dc * 8) : u32x4{0u, 0u, 0u, 0u};
+    for (int u = 0; u < LOADS; ++u) {
+      const int slot = (u * 4 + wave) * 64 + lane;
+      const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+      const size_t off = (size_t)min(j0 + row, T - 1) * N + cc * 8;
+      g2lds16(kg + off, kt + (u * 4 + wave) * 512);
+      g2lds16(vg + off, kt + TILE + (u * 4 + wave) * 512);
     }
   };
-  auto store = [&]() {
+
+  f32x16 dq[QB][DB];
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int id = tid + 256 * i, row = id / (N / 8), dc = id % (N / 8);
-      st16(Ks + row * KP + dc * 8, rk[i]);
-      st16(Vs + row * KP + dc * 8, rv[i]);
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) dq[qb][db] = zero16();
+
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int tr_row = 4 * h + (i16 >> 2);
+  const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+  const float sl2e = p.sl2e;
+
+  // One 32-key step of every query block of this wave. MASK: the step
+  // touches the causal diagonal or the end of the sequence.
+  auto step = [&](const bf16_bits* ks_t, const bf16_bits* vs_t, int st, int kb0, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    bf16x8 kf[KS], vf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int off = swz_off<CH>(st * 32 + c, 16 * ks + 8 * h);
+      kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + off));
+      vf[ks] = as_frag(*reinterpret_cast<const u32x4*>(vs_t + off));
     }
+    bf16x8 sf[QB][2];
 #pragma unroll
-    for (int i = 0; i < PCH; ++i) {
-      const int id = tid + 256 * i, rp = id / (N / 8), dc = id % (N / 8);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(Kt + (dc * 8) * TP + 2 * rp);
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qb0 = q0w + 32 * qb;
+      if (MASK && kb0 > qb0 + 31) {
+        sf[qb][0] = sf[qb][1] = as_frag(u32x4{0u, 0u, 0u, 0u});
+        continue;
+      }
+      f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t a = rp0[i][e], c = rp1[i][e];
-        dst[(2 * e) * TP / 2] = (a & 0xffffu) | (c << 16);
-        dst[(2 * e + 1) * TP / 2] = (a >> 16) | (c & 0xffff0000u);
+      for (int ks = 0; ks < KS; ++ks) {
+        s = mfma32(kf[ks], qf[qb][ks], s);
+        dp = mfma32(vf[ks], df[qb][ks], dp);
+      }
+      const int qq = qb0 + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float pv = fast_exp2(__builtin_fmaf(s[i], sl2e, -lse2[qb]));
+        if (MASK) {
+          const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
+          pv = (key > qq || key >= T) ? 0.f : pv;
+        }
+        s[i] = pv * (dp[i] - dlt[qb]);
+      }
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
+        sf[qb][kst] = as_frag(w);
+      }
+    }
+    // dQ^T += K^T dS^T, two 16-key MFMA steps.
+#pragma unroll
+    for (int kst = 0; kst < 2; ++kst) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int r = st * 32 + 16 * kst + tr_row, col = 32 * db + tr_col;
+        const bf16x8 kt = frag_from2(lds_read_tr4(ks_t + swz_off<CH>(r, col)), lds_read_tr4(ks_t + swz_off<CH>(r + 8, col)));
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          if (MASK && kb0 > q0w + 32 * qb + 31) continue;
+          dq[qb][db] = mfma32(kt, sf[qb][kst], dq[qb][db]);
+        }
       }
     }
   };
 
-  f32x4 dq[DB][2];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) dq[db][0] = dq[db][1] = zero4();
-
-  const int kv_end = min(T, q0 + BQ);
   const int nkv = (kv_end + BKV - 1) / BKV;
-  fetch(0);
-  for (int j = 0; j < nkv; ++j) {
-    store();
+  const int nfull = min(nkv, (qi * BQ) / BKV);
+  issue_tile(0, 0);
+  wait_vmcnt0();  // also retires the q/dO fragment loads
+  __syncthreads();
+  int j = 0;
+  for (; j < nfull; ++j) {
+    if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
+    const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
+    step(ks_t, ks_t + TILE, 0, j * BKV, std::false_type{});
+    step(ks_t, ks_t + TILE, 1, j * BKV + 32, std::false_type{});
+    wait_vmcnt0();
     __syncthreads();
-    if (j + 1 < nkv) fetch((j + 1) * BKV);
-    const int j0 = j * BKV;
-    if (j0 <= qw0 + QW - 1) {
-      f32x4 sa[4][2], pa[4][2];
+  }
+  for (; j < nkv; ++j) {
+    if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
+    const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        sa[kb][0] = sa[kb][1] = pa[kb][0] = pa[kb][1] = zero4();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const bf16x8 kf = as_frag(*reinterpret_cast<const u32x4*>(Ks + (kb * 16 + c16) * KP + s * 32 + 8 * g));
-          const bf16x8 vf = as_frag(*reinterpret_cast<const u32x4*>(Vs + (kb * 16 + c16) * KP + s * 32 + 8 * g));
-          sa[kb][0] = mfma(kf, qf[0][s], sa[kb][0]);
-          sa[kb][1] = mfma(kf, qf[1][s], sa[kb][1]);
-          pa[kb][0] = mfma(vf, df[0][s], pa[kb][0]);
-          pa[kb][1] = mfma(vf, df[1][s], pa[kb][1]);
-        }
-      }
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const int qq = qw0 + qb * 16 + c16;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = j0 + kb * 16 + 4 * g + r;
-            float pv = fast_exp2(sa[kb][qb][r] * p.sl2e - lse2[qb]);
-            if (key > qq || key >= T) pv = 0.f;
-            sa[kb][qb][r] = pv * (pa[kb][qb][r] - dlt[qb]);
-          }
-      }
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        bf16x8 sf[2];
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          u32x4 w;
-          w[0] = pack2(sa[2 * s2][qb][0], sa[2 * s2][qb][1]);
-          w[1] = pack2(sa[2 * s2][qb][2], sa[2 * s2][qb][3]);
-          w[2] = pack2(sa[2 * s2 + 1][qb][0], sa[2 * s2 + 1][qb][1]);
-          w[3] = pack2(sa[2 * s2 + 1][qb][2], sa[2 * s2 + 1][qb][3]);
-          sf[qb] = as_frag(w);
-        }
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const bf16_bits* kr = Kt + (db * 16 + c16) * TP + s2 * 32 + 4 * g;
-          const bf16x8 kt = frag_from2(*reinterpret_cast<const u32x2*>(kr), *reinterpret_cast<const u32x2*>(kr + 16));
-          dq[db][0] = mfma(kt, sf[0], dq[db][0]);
-          dq[db][1] = mfma(kt, sf[1], dq[db][1]);
-        }
-      }
+    for (int st = 0; st < 2; ++st) {
+      const int kb0 = j * BKV + st * 32;
+      if (kb0 <= q0w + QW - 1) step(ks_t, ks_t + TILE, st, kb0, std::true_type{});
     }
+    wait_vmcnt0();
     __syncthreads();
   }
 
   // Stage dQ (times the softmax scale) as fp32 rows, then the q chain.
-  float* stg = reinterpret_cast<float*>(smem) + wave * QW * FP;
+  float* stg = reinterpret_cast<float*>(smem_raw) + wave * QW * FP;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int db = 0; db < DB; ++db)
-      *reinterpret_cast<f32x4*>(stg + (qb * 16 + c16) * FP + db * 16 + 4 * g) = dq[db][qb] * p.scale;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x16& a = dq[qb][db];
+        const f32x4 v = {a[4 * r4], a[4 * r4 + 1], a[4 * r4 + 2], a[4 * r4 + 3]};
+        *reinterpret_cast<f32x4*>(stg + (32 * qb + c) * FP + 32 * db + 8 * r4 + 4 * h) = v * p.scale;
+      }
   __syncthreads();
-  head_row_bwd<N>(stg, FP, qw0, p, b, h, true, p.q, 1.0f / p.qscale, p.rq, p.daq);
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+    head_row_bwd<N>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, b, hd, true, p.q, 1.0f / p.qscale, p.rq, p.daq);
 }
 
 // ---------------------------------------------------------------------------
@@ -483,7 +517,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
 }
 
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
-  const int G = p.B * p.H * ((p.T + 127) / 128);
+  const int BQ = N == 64 ? 256 : 128;
+  const int G = p.B * p.H * ((p.T + BQ - 1) / BQ);
   if (N == 64)
     hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, dim3(G), dim3(256), 0, s, p);
   else

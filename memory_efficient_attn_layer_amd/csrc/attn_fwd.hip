@@ -201,23 +201,33 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     }
   };
 
+  // Tiles below the workgroup's first query need no mask for any wave and
+  // run in a branch-free loop; the (at most four) tiles of the diagonal
+  // region, and a ragged sequence end, follow in a second loop.
   auto main_loop = [&](auto fixed_tag) {
     const int nkv = (kv_end + BKV - 1) / BKV;
+    const int nfull = min(nkv, (qi * BQ) / BKV);
     issue_tile(0, 0);
     wait_vmcnt0();  // also retires the Q fragment loads
     __syncthreads();
-    for (int j = 0; j < nkv; ++j) {
+    int j = 0;
+    for (; j < nfull; ++j) {
+      if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
+      const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
+      const bf16_bits* vs_t = ks_t + TILE;
+      step(ks_t, vs_t, 0, j * BKV, fixed_tag, std::false_type{});
+      step(ks_t, vs_t, 1, j * BKV + 32, fixed_tag, std::false_type{});
+      wait_vmcnt0();
+      __syncthreads();
+    }
+    for (; j < nkv; ++j) {
       if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
       const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
       const bf16_bits* vs_t = ks_t + TILE;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         const int kb0 = j * BKV + st * 32;
-        if (kb0 > q0w + QW - 1) continue;  // every key of the step is in this wave's future
-        if (kb0 + 31 < q0w && kb0 + 32 <= T)
-          step(ks_t, vs_t, st, kb0, fixed_tag, std::false_type{});
-        else
-          step(ks_t, vs_t, st, kb0, fixed_tag, std::true_type{});
+        if (kb0 <= q0w + QW - 1) step(ks_t, vs_t, st, kb0, fixed_tag, std::true_type{});
       }
       wait_vmcnt0();
       __syncthreads();

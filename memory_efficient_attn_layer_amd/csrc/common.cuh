@@ -29,7 +29,9 @@ __device__ __forceinline__ f32x4 mfma(const bf16x8& a, const bf16x8& b, const f3
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+// Zero accumulators as splat constants, so a first MFMA can take the inline
+// constant 0 as its accumulator input instead of zeroed registers.
+__device__ __forceinline__ f32x4 zero4() { return (f32x4)(0.0f); }
 
 // v_mfma_f32_32x32x16_bf16, lane = 32*h + c (h in 0..1, c in 0..31):
 //   A operand (32 rows x 16 k): lane holds row c, k = 8h .. 8h+7
@@ -40,12 +42,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x16 zero16() {
-  f32x16 z;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) z[i] = 0.f;
-  return z;
-}
+__device__ __forceinline__ f32x16 zero16() { return (f32x16)(0.0f); }
 
 // LDS pointer types for the gfx950 LDS-only instructions.
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -97,8 +94,13 @@ __device__ __forceinline__ bf16_bits f2bf(float f) {
   __bf16 b = (__bf16)f;
   return __builtin_bit_cast(bf16_bits, b);
 }
+// Two fp32 -> packed bf16 pair with one v_cvt_pk_bf16_f32 (round to nearest
+// even).
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
@@ -116,8 +118,10 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
 }
 
 __device__ __forceinline__ bf16x8 as_frag(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+// Concatenation of two 64-bit halves into one MFMA operand; written as a
+// shuffle so the two halves can be loaded straight into adjacent registers.
 __device__ __forceinline__ bf16x8 frag_from2(const u32x2& a, const u32x2& b) {
-  u32x4 v = {a[0], a[1], b[0], b[1]};
+  const u32x4 v = __builtin_shufflevector(a, b, 0, 1, 2, 3);
   return __builtin_bit_cast(bf16x8, v);
 }
 
