@@ -304,8 +304,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 // ---------------------------------------------------------------------------
 // dK, dV
 //
-// One workgroup = one (batch, head) and BKV = 4*KW keys; wave w owns KW
-// consecutive keys (KW = 64 for N = 64, 32 for N = 128) whose K and V rows
+// One workgroup = one (batch, head) and BKV = 4*KW keys; wave w owns KW = 32
+// consecutive keys (two waves fit per SIMD) whose K and V rows
 // stay in registers as the B operands of
 //   S  = Q K^T   and   dP = dO V^T        (A = Q, dO rows from LDS)
 // on v_mfma_f32_32x32x16_bf16. The key index sits on the lane, so P and
@@ -317,8 +317,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 // block's first key (causal).
 // ---------------------------------------------------------------------------
 template <int N>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
-  constexpr int KW = N == 64 ? 64 : 32;  // keys per wave
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
+  constexpr int KW = 32;                 // keys per wave
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
   constexpr int BKV = 4 * KW;            // keys per workgroup
   constexpr int BQ = 64;                 // queries per LDS tile
@@ -527,7 +527,7 @@ hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
 }
 
 hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s) {
-  const int BKV = N == 64 ? 256 : 128;
+  const int BKV = 128;
   const int G = p.B * p.H * ((p.T + BKV - 1) / BKV);
   if (N == 64)
     hipLaunchKernelGGL(attn_bwd_dkdv_kernel<64>, dim3(G), dim3(256), 0, s, p);
