@@ -14,6 +14,7 @@
 // with acc = sum_p (rx da_p) W_p; neither xh nor dxh is ever stored.
 #include "gemm_core.cuh"
 #include "kernels.h"
+#include "slab.cuh"
 
 namespace mea {
 
@@ -157,86 +158,146 @@ hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// dx = rmsnorm_bwd([da_q|da_k|da_v|da_g] Wcat); one workgroup owns full rows.
+// dx = rmsnorm_bwd([da_q|da_k|da_v|da_g] Wcat), one workgroup owns full rows.
+//
+// Computed transposed, D^T = Wcat^T da^T: A = Wcat^T rows (C features, k =
+// 4HN contiguous), B = da rows (tokens). A workgroup covers all C features of
+// BT tokens with WF x WT waves of 128 features x 64 tokens; k-slabs of 32
+// stream through a 3-stage LDS ring filled by direct global->LDS loads. In
+// the accumulator layout a lane holds one token and 4 consecutive features,
+// so the RMSNorm backward dot (acc . x) is an in-lane sum, two lane
+// exchanges and a cross-wave sum through LDS; dx rows leave through an LDS
+// staging block as whole-row stores.
 // ---------------------------------------------------------------------------
 template <int C>
-__global__ __launch_bounds__(256) void dx_kernel(DxParams p) {
-  constexpr int BM = 32768 / C, BN = C;
-  constexpr int MB = BM / 16, NB = C / 64;
-  constexpr int XP = C + 8;
-  constexpr int SM_MAIN = NtSmem<BM, BN>::elems, SM_X = BM * XP;
-  __shared__ __attribute__((aligned(16))) bf16_bits smem[SM_MAIN > SM_X ? SM_MAIN : SM_X];
-  __shared__ float dotp[4][BM];
-  const int M = p.M, HN = p.HN, K4 = 4 * HN;
-  const int ntm = (M + BM - 1) / BM;
-  const int m0 = xcd_remap(blockIdx.x, ntm) * BM;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
+__global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 128) : 1)), 1) void dx_kernel(DxParams p) {
+  constexpr int WF = C / 128;                           // waves along features
+  constexpr int WT = 8 % WF == 0 ? 8 / WF : 1;          // waves along tokens
+  constexpr int NW = WF * WT;
+  constexpr int BT = 64 * WT;                           // tokens per workgroup
+  constexpr int BK = 32, NS = C * 2 <= 1024 ? 3 : 2;    // slab width, ring depth
+  constexpr int STAGE = (C + BT) * BK;
+  constexpr int FB = 8, TB = 4;                         // 16-blocks per wave
+  // Load instructions every wave issues per slab at least (waves whose
+  // share is larger wait for more of their own loads, which is still right).
+  constexpr int LOADS = (C / 16) / NW + (BT / 16) / NW;
+  constexpr int SP = 128 + 8;                           // staging pitch (elements)
+  __shared__ __attribute__((aligned(16))) bf16_bits smem[NS * STAGE];
+  __shared__ float dotp[WF][BT];
 
-  auto load_a = [&](int row, int k0, int kc, int) -> u32x4 {
-    const int m = m0 + row;
-    if (m >= M) return u32x4{0u, 0u, 0u, 0u};
-    return ld16(p.da + (size_t)m * K4 + k0 + kc * 8);
-  };
-  auto load_b = [&](int row, int k0, int kc, int) -> u32x4 {
-    return ld16(p.wcatT + (size_t)row * K4 + k0 + kc * 8);
-  };
-  f32x4 acc[MB][NB];
-  mainloop_nt<BM, BN, 1, 4>(K4, smem, load_a, load_b, acc);
+  const int M = p.M, K4 = 4 * p.HN;
+  const int m0 = xcd_remap(blockIdx.x, (M + BT - 1) / BT) * BT;
+  const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wf = wave % WF, wt = wave / WF;
+  const bf16_bits* wt_g = p.wcatT;  // (C, 4HN)
+  const bf16_bits* da = p.da;       // (M, 4HN)
 
-  // x tile -> LDS.
-  for (int id = tid; id < BM * (C / 8); id += 256) {
-    const int row = id / (C / 8), cc = id % (C / 8);
-    const int m = m0 + row;
-    const u32x4 v = m < M ? ld16(p.x + (size_t)m * C + cc * 8) : u32x4{0u, 0u, 0u, 0u};
-    st16(smem + row * XP + cc * 8, v);
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int ks, int st) {
+    const uint32_t lds = lds0 + (uint32_t)(st * STAGE) * 2u;
+    const int k0 = ks * BK;
+    slab_issue<C, NW, BK>(
+        lds, wave, K4, [&](int u) { return wt_g + (size_t)(u * NW * 16) * K4 + k0; }, [](int, int i) { return i; });
+    slab_issue<BT, NW, BK>(
+        lds + C * BK * 2, wave, K4,
+        [&](int u) { return da + (size_t)min(m0 + u * NW * 16, M - 1) * K4 + k0; },
+        [&](int u, int i) { return min(m0 + u * NW * 16 + i, M - 1) - min(m0 + u * NW * 16, M - 1); });
+  };
+
+  f32x4 acc[FB][TB];
+#pragma unroll
+  for (int fb = 0; fb < FB; ++fb)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = zero4();
+
+  // Ring of NS stages, NS - 1 slabs in flight ahead of the one multiplied.
+  const int nk = K4 / BK;
+  for (int s0 = 0; s0 < NS - 1 && s0 < nk; ++s0) issue(s0, s0);
+  for (int ks = 0; ks < nk; ++ks) {
+    if (NS == 3 && ks + 1 < nk)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);  // vmcnt(LOADS): only slab ks + 1 may be pending
+    else
+      wait_vmcnt0();
+    __syncthreads();
+    if (ks + NS - 1 < nk) issue(ks + NS - 1, (ks + NS - 1) % NS);
+    const bf16_bits* As = smem + (ks % NS) * STAGE;
+    const bf16_bits* Bs = As + C * BK;
+    bf16x8 af[FB], bfr[TB];
+#pragma unroll
+    for (int fb = 0; fb < FB; ++fb) af[fb] = as_frag(slab_read<BK>(As, wf * 128 + fb * 16 + c16, g));
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) bfr[tb] = as_frag(slab_read<BK>(Bs, wt * 64 + tb * 16 + c16, g));
+#pragma unroll
+    for (int fb = 0; fb < FB; ++fb)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = mfma(af[fb], bfr[tb], acc[fb][tb]);
   }
-  __syncthreads();
-  const int col0 = wave * (C / 4);
+
+  // acc . x over this wave's 128 features, per token, then across the WF
+  // waves that share the tokens.
+  const bf16_bits* xg = p.x;
+  int mrow[TB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int tb = 0; tb < TB; ++tb) {
+    mrow[tb] = min(m0 + wt * 64 + tb * 16 + c16, M - 1);
+    float d = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = mb * 16 + 4 * g + r;
-      float s = 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) s += acc[mb][nb][r] * bf2f(smem[row * XP + col0 + nb * 16 + c16]);
-      s = sum16(s);
-      if (c16 == 0) dotp[wave][row] = s;
+    for (int fb = 0; fb < FB; ++fb) {
+      const u32x2 xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + wf * 128 + 16 * fb + 4 * g);
+      d += acc[fb][tb][0] * lo_bf(xv[0]) + acc[fb][tb][1] * hi_bf(xv[0]) + acc[fb][tb][2] * lo_bf(xv[1]) +
+           acc[fb][tb][3] * hi_bf(xv[1]);
     }
-  __syncthreads();
+    d += shfl_xor(d, 16);
+    d += shfl_xor(d, 32);
+    if (g == 0) dotp[wf][wt * 64 + tb * 16 + c16] = d;
+  }
+  __syncthreads();  // also: every wave is past its last slab read
+
+  // dx = acc - x rx^2 (acc . x) / C, staged per 16-token block and stored as
+  // whole 256-byte row segments.
+  bf16_bits* stg = smem + wave * 16 * SP;
+  const float inv_c = 1.0f / (float)C;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int tb = 0; tb < TB; ++tb) {
+    const int tl = wt * 64 + tb * 16 + c16;
+    float dot = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = mb * 16 + 4 * g + r;
-      const int m = m0 + row;
-      const float rxv = m < M ? p.rx[m] : 0.f;
-      const float dot = dotp[0][row] + dotp[1][row] + dotp[2][row] + dotp[3][row];
-      const float cf = rxv * rxv * dot / (float)C;
+    for (int i = 0; i < WF; ++i) dot += dotp[i][tl];
+    const float rxv = p.rx[mrow[tb]];
+    const float cf = rxv * rxv * dot * inv_c;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        bf16_bits& xr = smem[row * XP + col0 + nb * 16 + c16];
-        xr = f2bf(acc[mb][nb][r] - bf2f(xr) * cf);
-      }
+    for (int fb = 0; fb < FB; ++fb) {
+      const u32x2 xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + wf * 128 + 16 * fb + 4 * g);
+      const f32x4& a = acc[fb][tb];
+      const float o0 = a[0] - lo_bf(xv[0]) * cf, o1 = a[1] - hi_bf(xv[0]) * cf;
+      const float o2 = a[2] - lo_bf(xv[1]) * cf, o3 = a[3] - hi_bf(xv[1]) * cf;
+      *reinterpret_cast<u32x2*>(stg + c16 * SP + 16 * fb + 4 * g) = u32x2{pack2(o0, o1), pack2(o2, o3)};
     }
-  __syncthreads();
-  for (int id = tid; id < BM * (C / 8); id += 256) {
-    const int row = id / (C / 8), cc = id % (C / 8);
-    const int m = m0 + row;
-    if (m < M) st16(p.dx + (size_t)m * C + cc * 8, *reinterpret_cast<const u32x4*>(smem + row * XP + cc * 8));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+#pragma unroll
+    for (int it = 0; it < 16 * 16 / 64; ++it) {
+      const int id = lane + 64 * it, row = id >> 4, ch = id & 15;
+      const int m = m0 + wt * 64 + tb * 16 + row;
+      const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * SP + ch * 8);
+      if (m < M) st16(p.dx + (size_t)m * C + wf * 128 + ch * 8, val);
+    }
   }
 }
 
 hipError_t launch_dx(const DxParams& p, hipStream_t s) {
   switch (p.C) {
     case 256:
-      hipLaunchKernelGGL(dx_kernel<256>, dim3((p.M + 127) / 128), dim3(256), 0, s, p);
+      hipLaunchKernelGGL(dx_kernel<256>, dim3((p.M + 255) / 256), dim3(512), 0, s, p);
       break;
     case 512:
-      hipLaunchKernelGGL(dx_kernel<512>, dim3((p.M + 63) / 64), dim3(256), 0, s, p);
+      hipLaunchKernelGGL(dx_kernel<512>, dim3((p.M + 127) / 128), dim3(512), 0, s, p);
+      break;
+    case 768:
+      hipLaunchKernelGGL(dx_kernel<768>, dim3((p.M + 63) / 64), dim3(384), 0, s, p);
       break;
     case 1024:
-      hipLaunchKernelGGL(dx_kernel<1024>, dim3((p.M + 31) / 32), dim3(256), 0, s, p);
+      hipLaunchKernelGGL(dx_kernel<1024>, dim3((p.M + 63) / 64), dim3(512), 0, s, p);
       break;
     default:
       return hipErrorInvalidValue;

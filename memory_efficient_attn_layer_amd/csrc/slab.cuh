@@ -26,24 +26,26 @@ __device__ __forceinline__ int slab_swz(int row) {
 }
 
 // Issues the loads of an R-row slab into LDS byte address lds, shared by the
-// NW waves of the workgroup. Rows come in groups of G = NW * 64 / CH (the
-// rows one round of load instructions covers): group u starts at the
-// wave-uniform address base(u) (element k0 of its first row) and its row i
-// (0 <= i < G) is read from row row_of(u, i) >= 0 of that base, rows being
-// stride elements apart. Callers clamp rows past the end of their matrix
-// inside row_of.
+// NW waves of the workgroup. One load instruction covers RPI = 64 / CH rows;
+// rows come in groups of G = NW * RPI (one round of instructions, the last
+// round possibly partial): group u starts at the wave-uniform address base(u)
+// (element k0 of its first row) and its row i (0 <= i < G) is read from row
+// row_of(u, i) >= 0 of that base, rows being stride elements apart. Callers
+// clamp rows past the end of their matrix inside row_of.
 template <int R, int NW, int KS, class Base, class RowOf>
 __device__ __forceinline__ void slab_issue(uint32_t lds, int wave, int stride, Base base, RowOf row_of) {
-  constexpr int CH = KS / 8, RPI = 64 / CH, G = NW * RPI;
-  static_assert(R % G == 0, "slab rows");
+  constexpr int CH = KS / 8, RPI = 64 / CH, NI = R / RPI;
+  static_assert(R % RPI == 0, "slab rows");
   const int lane = threadIdx.x & 63;
   const int i = wave * RPI + lane / CH;
 #pragma unroll
-  for (int u = 0; u < R / G; ++u) {
-    const int row = u * G + i;
+  for (int u = 0; u < (NI + NW - 1) / NW; ++u) {
+    const int ins = u * NW + wave;
+    if (NI % NW != 0 && ins >= NI) break;  // wave-uniform: partial last round
+    const int row = ins * RPI + lane / CH;
     const int chunk = (lane % CH) ^ slab_swz<KS>(row);
     const uint32_t voff = (uint32_t)(row_of(u, i) * stride + chunk * 8) * 2u;
-    g2lds16_s(base(u), voff, lds + (uint32_t)(u * NW + wave) * 1024u);
+    g2lds16_s(base(u), voff, lds + (uint32_t)ins * 1024u);
   }
 }
 

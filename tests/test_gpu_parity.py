@@ -93,6 +93,7 @@ BLOCK_CASES = [
     ("t1-b2", _w("t1", 2, 1, 256, 4, 64), None),
     ("t129-b1", _w("t129", 1, 129, 512, 8, 64), None),
     ("c-ne-hn-b2-t160", _w("chn", 2, 160, 512, 4, 64), None),
+    ("c768-b1-t100", _w("c768", 1, 100, 768, 4, 64), None),
     ("yarn8-b2-t300-n128", _w("y8", 2, 300, 256, 2, 128, 8.0, 64), None),
 ]
 
