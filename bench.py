@@ -13,6 +13,7 @@ timed region), peak HBM, and the CPU baseline (the fp32 oracle on a bounded
 batch slice on the host cores). Progress goes to stderr.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--compare-eager] [--no-cpu-baseline]
+    python bench.py --copy-calibration   # a plain 256 MiB device copy, for HBM counter scaling
 """
 from __future__ import annotations
 
@@ -48,7 +49,7 @@ def kernel_work(w):
         "attn_fwd": dict(flops=2 * pair, bytes=2.0 * 4 * M * HN),
         "gate_oproj": dict(flops=2.0 * M * HN * C, bytes=2.0 * 2 * M * HN + 2.0 * M * C),
         "dz_gate_bwd": dict(flops=2.0 * M * C * HN, bytes=2.0 * M * C + 2.0 * 4 * M * HN),
-        "attn_bwd_dq": dict(flops=1 * pair, bytes=2.0 * 3 * M * HN),
+        "attn_bwd_dq": dict(flops=1 * pair, bytes=2.0 * 5 * M * HN),
         "attn_bwd_dkdv": dict(flops=3 * pair, bytes=2.0 * 6 * M * HN),
         "dw_partial": dict(flops=2.0 * M * (4 * HN * C + C * HN), bytes=2.0 * M * (4 * HN + C + C + 2 * HN)),
         "dx": dict(flops=2.0 * M * 4 * HN * C, bytes=2.0 * M * (4 * HN + 2 * C)),
@@ -148,6 +149,8 @@ def main():
     ap.add_argument("--compare-eager", action="store_true", help="also time the eager SDPA path on the GPU")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of 256 MiB five times (reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported; this block runs on one GPU only "
@@ -155,6 +158,16 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
+        return
 
     from memory_efficient_attn_layer_amd import _lib
     from memory_efficient_attn_layer_amd.attention import FusedAttentionFunction
@@ -214,6 +227,19 @@ def main():
             traffic = None
     roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
+    # The three attention kernels together: algorithmic flops (forward 2, backward
+    # 4 causal products) and the products the hardware runs (the backward
+    # recomputes S twice and dP once more).
+    attn = ("attn_fwd", "attn_bwd_dq", "attn_bwd_dkdv")
+    if all(k in prof for k in attn):
+        pair = work["attn_bwd_dq"]["flops"]
+        t_attn = sum(prof[k][1] / prof[k][0] for k in attn) * 1e-3
+        attention = {"ms": round(t_attn * 1e3, 4), "alg_tflops": round(6 * pair / t_attn / 1e12, 2),
+                     "alg_frac": round(6 * pair / t_attn / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "hw_tflops": round(9 * pair / t_attn / 1e12, 2),
+                     "hw_frac": round(9 * pair / t_attn / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    else:
+        attention = None
 
     eager = None
     if args.compare_eager:
@@ -255,6 +281,7 @@ def main():
         "peak_hbm": {"fused_bytes": int(peak), "eager_sdpa": eager},
         "block_tflops": round(3 * w.flops_fwd() / sec / 1e12, 2),
         "roofline": roofline,
+        "attention": attention,
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
