@@ -168,13 +168,26 @@ __device__ __forceinline__ float fast_sigmoid(float a) {
 }
 
 // Row-major bf16 tiles in LDS are stored as 16-byte chunks; chunk c of row r
-// sits at chunk slot c ^ swz(r) of that row. For rows of 8 chunks (128 B)
-// two rows share one 256-byte bank line, so 16 consecutive rows read at one
-// chunk index hit 16 distinct 16-byte bank groups; likewise for 16-chunk rows.
+// sits at chunk slot c ^ swz(r). Two access patterns must be conflict-free:
+//  - 16-byte row reads: 16 lanes read one chunk of 16 consecutive rows. For
+//    rows of 8 chunks (128 B) two rows share a 256-byte bank line, so the 8
+//    rows of each parity need distinct swizzles: p = (r >> 1) & 7 does that.
+//    For rows of 16 chunks any permutation of r & 15 does.
+//  - transposing 8-byte reads (ds_read_b64_tr_b16): 64 lanes read 4 aligned
+//    chunks of 8 consecutive rows. The swizzle's bit 2 (8-chunk rows, over row
+//    pairs) or bits 2-3 (16-chunk rows, over rows) must then take each value
+//    equally often, so the 4-chunk groups of the rows spread over the whole
+//    bank line instead of stacking on one quarter of it.
+// p ^ ((p & 1) << 2) and r ^ ((r & 3) << 2) satisfy both.
 template <int CH>
 __device__ __forceinline__ int chunk_swz(int row) {
   static_assert(CH == 8 || CH == 16, "rows of 64 or 128 bf16");
-  return CH == 8 ? ((row >> 1) & 7) : (row & 15);
+  if (CH == 8) {
+    const int p = (row >> 1) & 7;
+    return p ^ ((p & 1) << 2);
+  }
+  const int r = row & 15;
+  return r ^ ((r & 3) << 2);
 }
 // Element offset of (row, col) in a swizzled tile with CH chunks per row.
 template <int CH>
