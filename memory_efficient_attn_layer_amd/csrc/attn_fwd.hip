@@ -87,15 +87,37 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     for (int ks = 0; ks < KS; ++ks) qf[qb][ks] = as_frag(ld16(p.q + head_off + (size_t)t * N + 16 * ks + 8 * h));
   }
 
-  auto issue_tile = [&](int j0, int stage) {
-    bf16_bits* kt = smem + stage * 2 * TILE;
+  // Tile loads: lane L of load u fills 16-byte slot L of row block u*4+wave;
+  // its row and swizzled chunk are fixed, so a whole tile is fetched from a
+  // wave-uniform base (row j0) plus a lane-constant byte offset. Only a tile
+  // that runs past the sequence end takes per-lane clamped addresses.
+  uint32_t ld_row[LOADS], ld_off[LOADS];
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int slot = (u * 4 + wave) * 64 + lane;
-      const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
-      const size_t off = (size_t)min(j0 + row, T - 1) * N + cc * 8;
-      g2lds16(kg + off, kt + (u * 4 + wave) * 512);
-      g2lds16(vg + off, kt + TILE + (u * 4 + wave) * 512);
+  for (int u = 0; u < LOADS; ++u) {
+    const int slot = (u * 4 + wave) * 64 + lane;
+    const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+    ld_row[u] = row;
+    ld_off[u] = (uint32_t)(row * N + cc * 8) * 2u;
+  }
+  const uint32_t smem_b = lds_addr(smem);
+  auto issue_tile = [&](int j0, int stage) {
+    const uint32_t kt = smem_b + (uint32_t)(stage * 2 * TILE) * 2u;
+    if (j0 + BKV <= T) {
+      const bf16_bits* kb = kg + (size_t)j0 * N;
+      const bf16_bits* vb = vg + (size_t)j0 * N;
+#pragma unroll
+      for (int u = 0; u < LOADS; ++u) {
+        g2lds16_s(kb, ld_off[u], kt + (uint32_t)(u * 4 + wave) * 1024u);
+        g2lds16_s(vb, ld_off[u], kt + (uint32_t)(TILE * 2) + (uint32_t)(u * 4 + wave) * 1024u);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < LOADS; ++u) {
+        const int row = min(j0 + (int)ld_row[u], T - 1);
+        const uint32_t off = ld_off[u] + (uint32_t)((row - j0 - (int)ld_row[u]) * N) * 2u;
+        g2lds16_s(kg + (size_t)j0 * N, off, kt + (uint32_t)(u * 4 + wave) * 1024u);
+        g2lds16_s(vg + (size_t)j0 * N, off, kt + (uint32_t)(TILE * 2) + (uint32_t)(u * 4 + wave) * 1024u);
+      }
     }
   };
 
@@ -109,10 +131,30 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     for (int db = 0; db < DB; ++db) o[qb][db] = zero16();
   }
 
-  // Lane-dependent parts of the fragment addresses.
+  // Lane-constant parts of the fragment addresses (elements). The swizzle of
+  // a row depends on row & 15 only, so the step (32 rows) and k-step (16
+  // rows) parts of an address are plain offsets.
   const int g16 = lane >> 4, i16 = lane & 15;
-  const int tr_row = 4 * h + (i16 >> 2);             // + 16*kstep + 8*t (+ 32*st)
+  const int tr_row = 4 * h + (i16 >> 2);             // + 16*kstep + 8*x (+ 32*st)
   const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);  // + 32*db
+  int koff[KS], voff[2][DB];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = swz_off<CH>(c, 16 * ks + 8 * h);
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) voff[x][db] = swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col);
+
+  // Row sums of P on the matrix core: a 16x16x32 MFMA with B = the P^T
+  // fragment of one 16-key MFMA step sees, in lane 16g + n, query n + 16(g&1)
+  // and the keys of half g >> 1. With A row m selecting the groups with
+  // g & 1 == m, D row 0 (1) of column n is the sum of P over those 16 keys for
+  // query n (n + 16): lanes 0..15, registers 0 and 1.
+  const uint32_t selw = (i16 == (g16 & 1)) ? 0x3F803F80u : 0u;
+  const bf16x8 sel = as_frag(u32x4{selw, selw, selw, selw});
+  f32x4 lsum[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) lsum[qb] = zero4();
 
   // One 32-key step of every query block of this wave. FIXED: exp2 of the
   // raw logit; otherwise the online form. MASK: the step touches the causal
@@ -123,7 +165,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     bf16x8 kf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + swz_off<CH>(st * 32 + c, 16 * ks + 8 * h)));
+      kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + st * 32 * N + koff[ks]));
     bf16x8 pf[QB][2];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -147,11 +189,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
       float ls = 0.f;
       if (FIXED) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = fast_exp2(s[i]);
-          s[i] = e;
-          ls += e;
-        }
+        for (int i = 0; i < 16; ++i) s[i] = fast_exp2(s[i]);
       } else {
         float mx = s[0];
 #pragma unroll
@@ -175,13 +213,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
           ls += e;
         }
       }
-      l_i[qb] += ls;
+      if (!FIXED) l_i[qb] += ls;
 #pragma unroll
       for (int kst = 0; kst < 2; ++kst) {
         u32x4 w;
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
         pf[qb][kst] = as_frag(w);
+        if (FIXED) lsum[qb] = mfma(sel, pf[qb][kst], lsum[qb]);
       }
     }
     // O^T += V^T P^T, two 16-key MFMA steps.
@@ -189,9 +228,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     for (int kst = 0; kst < 2; ++kst) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const int r = st * 32 + 16 * kst + tr_row, col = 32 * db + tr_col;
-        const bf16x8 vf = frag_from2(lds_read_tr4(vs_t + swz_off<CH>(r, col)),
-                                     lds_read_tr4(vs_t + swz_off<CH>(r + 8, col)));
+        const bf16_bits* vr = vs_t + (st * 32 + 16 * kst) * N;
+        const bf16x8 vf = frag_from2(lds_read_tr4(vr + voff[0][db]), lds_read_tr4(vr + voff[1][db]));
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           if (MASK && kb0 > q0w + 32 * qb + 31) continue;
@@ -199,6 +237,85 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
         }
       }
     }
+  };
+
+  // A whole unmasked 64-key tile in the fixed-offset form (two query blocks
+  // per wave), written as a software pipeline over its four 32x32 blocks
+  // (step st, query block qb): the exp2 / convert work of one block is
+  // issued between the MFMAs of the next block's S^T and of the previous
+  // block's O^T update, so one wave keeps the matrix core fed while its own
+  // VALU work runs. Phases are fenced with sched_barrier and interleaved with
+  // sched_group_barrier patterns (MFMA, VALU, DS read).
+  auto tile_fixed = [&](const bf16_bits* ks_t, const bf16_bits* vs_t, auto fixed_tag) {
+    static_assert(decltype(fixed_tag)::value && QB == 2, "fixed offset, two query blocks per wave");
+    bf16x8 kf[2][KS], vf[2][2][DB], pf[2][2][2];
+    f32x16 s[2][2];
+    auto load_k = [&](int st) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        kf[st][ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + st * 32 * N + koff[ks]));
+    };
+    auto load_v = [&](int st) {
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const bf16_bits* vr = vs_t + (st * 32 + 16 * kst) * N;
+          vf[st][kst][db] = frag_from2(lds_read_tr4(vr + voff[0][db]), lds_read_tr4(vr + voff[1][db]));
+        }
+    };
+    auto S = [&](int st, int qb) {
+      s[st][qb] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s[st][qb] = mfma32(kf[st][ks], qf[qb][ks], s[st][qb]);
+    };
+    auto E = [&](int st, int qb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[st][qb][i] = fast_exp2(s[st][qb][i]);
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = pack2(s[st][qb][8 * kst + 2 * e], s[st][qb][8 * kst + 2 * e + 1]);
+        pf[st][qb][kst] = as_frag(w);
+      }
+    };
+    auto PV = [&](int st, int qb) {
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[qb][db] = mfma32(vf[st][kst][db], pf[st][qb][kst], o[qb][db]);
+        lsum[qb] = mfma(sel, pf[st][qb][kst], lsum[qb]);
+      }
+    };
+    constexpr int PVM = 2 * DB + 2;  // MFMAs of one PV()
+    load_k(0);
+    S(0, 0);
+    load_v(0);
+    load_k(1);
+    __builtin_amdgcn_sched_barrier(0);
+    S(0, 1);
+    E(0, 0);
+    sched_pattern<KS, 1, 24 / KS, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    PV(0, 0);
+    S(1, 0);
+    E(0, 1);
+    load_v(1);
+    sched_pattern<8, 1, 3, 1>();
+    sched_pattern<1, PVM + KS - 8, 0, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    PV(0, 1);
+    S(1, 1);
+    E(1, 0);
+    sched_pattern<8, 1, 3, 0>();
+    sched_pattern<1, PVM + KS - 8, 0, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    PV(1, 0);
+    E(1, 1);
+    sched_pattern<PVM, 1, 24 / PVM, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    PV(1, 1);
   };
 
   // Tiles below the workgroup's first query need no mask for any wave and
@@ -215,8 +332,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
       if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
       const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
       const bf16_bits* vs_t = ks_t + TILE;
-      step(ks_t, vs_t, 0, j * BKV, fixed_tag, std::false_type{});
-      step(ks_t, vs_t, 1, j * BKV + 32, fixed_tag, std::false_type{});
+      if constexpr (decltype(fixed_tag)::value && QB == 2) {
+        tile_fixed(ks_t, vs_t, fixed_tag);
+      } else {
+        step(ks_t, vs_t, 0, j * BKV, fixed_tag, std::false_type{});
+        step(ks_t, vs_t, 1, j * BKV + 32, fixed_tag, std::false_type{});
+      }
       wait_vmcnt0();
       __syncthreads();
     }
@@ -233,10 +354,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
       __syncthreads();
     }
   };
-  if (fixed)
+  if (fixed) {
     main_loop(std::true_type{});
-  else
+    // Row sums from the MFMA accumulators (lanes 0..15), spread so that both
+    // halves h of each query column see the whole sum in l_i.
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float v0 = __shfl(lsum[qb][0], c & 15, 64), v1 = __shfl(lsum[qb][1], c & 15, 64);
+      l_i[qb] = h == 0 ? (c < 16 ? v0 : v1) : 0.f;
+    }
+  } else {
     main_loop(std::false_type{});
+  }
 
   // Normalise, write lse and stage O^T (lane = query) as rows for 16-byte stores.
   bf16_bits* stg = smem + wave * QW * OP;
