@@ -12,100 +12,107 @@
 // Projection-gradient rows arrive pre-scaled by rx = 1/rms(x), so
 //   dW_p = (rx da_p)^T x   and   dx = acc - x * rx^2 * (acc . x) / C
 // with acc = sum_p (rx da_p) W_p; neither xh nor dxh is ever stored.
-#include "gemm_core.cuh"
 #include "kernels.h"
 #include "slab.cuh"
+#include "tokgemm.cuh"
 
 namespace mea {
 
 // ---------------------------------------------------------------------------
-// y = (O * sig) Wo^T
+// y = (O * sig) Wo^T, on the token-block main loop: A = Wo rows (output
+// features, k = HN), B = O * sig rows, gated while the slab is written to
+// LDS. Workgroup (x, y) covers the NF output features from y * NF of BT
+// tokens; y rows leave through an LDS staging block as whole-row segments.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gate_oproj_kernel(OprojParams p) {
-  constexpr int BM = 128, BN = 256, SP = BN + 8;
-  constexpr int SM_MAIN = NtSmem<BM, BN>::elems, SM_STG = BM * SP;
-  __shared__ __attribute__((aligned(16))) bf16_bits smem[SM_MAIN > SM_STG ? SM_MAIN : SM_STG];
+template <int NF>
+__global__ __launch_bounds__(TokShape<NF>::NT, 1) void gate_oproj_kernel(OprojParams p) {
+  using S = TokShape<NF>;
+  constexpr int SP = 128 + 8;  // staging pitch (elements)
+  static_assert(S::NW * 16 * SP <= S::SMEM, "staging fits the slab stages");
+  __shared__ __attribute__((aligned(16))) bf16_bits smem[S::SMEM];
   const int M = p.M, C = p.C, HN = p.HN;
-  const int nct = C / BN, ntm = (M + BM - 1) / BM;
-  const int L = xcd_remap(blockIdx.x, ntm * nct);
-  const int m0 = (L / nct) * BM, n0 = (L % nct) * BN;
-  const int tid = threadIdx.x, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  const int m0 = xcd_remap(blockIdx.x, gridDim.x) * S::BT, f0 = blockIdx.y * NF;
+  f32x4 acc[8][4];
+  tok_mainloop<NF, true>(HN, smem, p.wo + (size_t)f0 * HN, HN, NF, p.o, p.sig, HN, m0, M, acc);
 
-  auto load_a = [&](int row, int k0, int kc, int) -> u32x4 {
-    const int m = m0 + row;
-    if (m >= M) return u32x4{0u, 0u, 0u, 0u};
-    const size_t off = (size_t)m * HN + k0 + kc * 8;
-    float o[8], s[8];
-    unpack8(ld16(p.o + off), o);
-    unpack8(ld16(p.sig + off), s);
+  const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
+  const int wave = tid >> 6, wf = wave % S::WF, wt = wave / S::WF;
+  bf16_bits* stg = smem + wave * 16 * SP;  // the main loop ended on a barrier
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] *= s[i];
-    return pack8(o);
-  };
-  auto load_b = [&](int row, int k0, int kc, int) -> u32x4 {
-    return ld16(p.wo + (size_t)(n0 + row) * HN + k0 + kc * 8);
-  };
-  f32x4 acc[4][8];
-  mainloop_nt<BM, BN, 2, 2>(HN, smem, load_a, load_b, acc);
-
-  stage_acc_bf16<4, 8, SP>(smem, wm * 64, wn * 128, acc, [](int, int, float v) { return v; });
-  __syncthreads();
-#pragma unroll 4
-  for (int it = 0; it < BM * (BN / 8) / 256; ++it) {
-    const int id = tid + 256 * it, row = id / (BN / 8), cc = id % (BN / 8);
-    const int m = m0 + row;
-    if (m < M) st16(p.y + (size_t)m * C + n0 + cc * 8, *reinterpret_cast<const u32x4*>(smem + row * SP + cc * 8));
+  for (int tb = 0; tb < S::TB; ++tb) {
+#pragma unroll
+    for (int fb = 0; fb < S::FB; ++fb) {
+      const f32x4& a = acc[fb][tb];
+      *reinterpret_cast<u32x2*>(stg + c16 * SP + 16 * fb + 4 * g) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+#pragma unroll
+    for (int it = 0; it < 16 * 16 / 64; ++it) {
+      const int id = lane + 64 * it, row = id >> 4, ch = id & 15;
+      const int m = m0 + wt * 64 + tb * 16 + row;
+      const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * SP + ch * 8);
+      if (m < M) st16(p.y + (size_t)m * C + f0 + wf * 128 + ch * 8, val);
+    }
   }
 }
 
+template <int NF>
+static void launch_oproj_nf(const OprojParams& p, hipStream_t s) {
+  const dim3 grid((p.M + TokShape<NF>::BT - 1) / TokShape<NF>::BT, p.C / NF);
+  hipLaunchKernelGGL(gate_oproj_kernel<NF>, grid, dim3(TokShape<NF>::NT), 0, s, p);
+}
+
 hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s) {
-  const int G = ((p.M + 127) / 128) * (p.C / 256);
-  hipLaunchKernelGGL(gate_oproj_kernel, dim3(G), dim3(256), 0, s, p);
+  if (p.C % 256 != 0 || p.HN % 32 != 0) return hipErrorInvalidValue;
+  if (p.C == 256)
+    launch_oproj_nf<256>(p, s);
+  else if (p.C == 768)
+    launch_oproj_nf<768>(p, s);
+  else if (p.C == 1024)
+    launch_oproj_nf<1024>(p, s);
+  else if (p.C % 512 == 0)
+    launch_oproj_nf<512>(p, s);
+  else
+    launch_oproj_nf<256>(p, s);
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// dZ = dy Wo with the gate backward in the epilogue.
+// dZ = dy Wo with the gate backward in the epilogue, on the token-block main
+// loop: A = Wo^T rows (HN features, k = C), B = dy rows. Workgroup (x, y)
+// covers features y * NF .. y * NF + NF - 1 (clamped to HN; groups hold whole
+// heads since NF is a multiple of N) of BT tokens. Each wave stages its fp32
+// dZ block per 16 tokens and walks it as rows: lane (row, 8-feature chunk)
+// loads sig and O, writes dO into the head-major (B, H, T, N) layout, da_g,
+// z = O * sig over sig, and delta = rowsum(dO * O) per (token, head), summed
+// over the N / 8 lanes of the head.
 // ---------------------------------------------------------------------------
-template <int N>
-__global__ __launch_bounds__(256) void dz_gate_bwd_kernel(DzParams p) {
-  constexpr int BM = 128, BN = 256, FP = 128 + 4;
-  constexpr int SM_MAIN = NtSmem<BM, BN>::elems * 2, SM_STG = 4 * 32 * FP * 4;  // bytes
-  __shared__ __attribute__((aligned(16))) unsigned char smem[SM_MAIN > SM_STG ? SM_MAIN : SM_STG];
-  const int M = p.M, C = p.C, H = p.H, T = p.T, HN = H * N;
-  const int nct = (HN + BN - 1) / BN, ntm = (M + BM - 1) / BM;
-  const int L = xcd_remap(blockIdx.x, ntm * nct);
-  const int m0 = (L / nct) * BM, n0 = (L % nct) * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-  const int c16 = lane & 15, g = lane >> 4;
+template <int NF>
+__global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzParams p) {
+  using S = TokShape<NF>;
+  constexpr int FP = 128 + 4;  // fp32 staging pitch
+  constexpr int SM_BYTES = S::SMEM * 2 > S::NW * 16 * FP * 4 ? S::SMEM * 2 : S::NW * 16 * FP * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SM_BYTES];
+  const int M = p.M, C = p.C, H = p.H, T = p.T, N = p.N, HN = H * N;
+  const int m0 = xcd_remap(blockIdx.x, gridDim.x) * S::BT, f0 = blockIdx.y * NF;
+  f32x4 acc[8][4];
+  tok_mainloop<NF, false>(C, reinterpret_cast<bf16_bits*>(smem), p.woT + (size_t)f0 * C, C, HN - f0, p.dy, nullptr,
+                          C, m0, M, acc);
 
-  auto load_a = [&](int row, int k0, int kc, int) -> u32x4 {
-    const int m = m0 + row;
-    return m < M ? ld16(p.dy + (size_t)m * C + k0 + kc * 8) : u32x4{0u, 0u, 0u, 0u};
-  };
-  auto load_b = [&](int row, int k0, int kc, int) -> u32x4 {
-    const int j = n0 + row;
-    return j < HN ? ld16(p.woT + (size_t)j * C + k0 + kc * 8) : u32x4{0u, 0u, 0u, 0u};
-  };
-  f32x4 acc[4][8];
-  mainloop_nt<BM, BN, 2, 2>(C, reinterpret_cast<bf16_bits*>(smem), load_a, load_b, acc);
-
-  float* stg = reinterpret_cast<float*>(smem) + wave * 32 * FP;
-  constexpr int CPH = N / 8;  // 16-byte chunks per head row
+  const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
+  const int wave = tid >> 6, wf = wave % S::WF, wt = wave / S::WF;
+  float* stg = reinterpret_cast<float*>(smem) + wave * 16 * FP;  // the main loop ended on a barrier
 #pragma unroll
-  for (int hf = 0; hf < 2; ++hf) {
+  for (int tb = 0; tb < S::TB; ++tb) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int fb = 0; fb < S::FB; ++fb)
+      *reinterpret_cast<f32x4*>(stg + c16 * FP + 16 * fb + 4 * g) = acc[fb][tb];
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) stg[(mb * 16 + 4 * g + r) * FP + nb * 16 + c16] = acc[2 * hf + mb][nb][r];
-    __syncthreads();
-#pragma unroll 1
-    for (int pass = 0; pass < 8; ++pass) {
-      const int row = pass * 4 + (lane >> 4), cc = lane & 15;
-      const int m = m0 + wm * 64 + hf * 32 + row;
-      const int j = n0 + wn * 128 + cc * 8;
+    for (int it = 0; it < 4; ++it) {
+      const int row = it * 4 + (lane >> 4), cc = lane & 15;
+      const int m = m0 + wt * 64 + tb * 16 + row;
+      const int j = f0 + wf * 128 + cc * 8;
       const bool valid = m < M && j < HN;
       const int mc = m < M ? m : M - 1, jc = j < HN ? j : 0;
       float dz[8], sg[8], ov[8];
@@ -132,9 +139,9 @@ __global__ __launch_bounds__(256) void dz_gate_bwd_kernel(DzParams p) {
       dl += xor1(dl);
       dl += xor2(dl);
       dl += shfl_xor(dl, 4);
-      if (CPH == 16) dl += shfl_xor(dl, 8);
+      if (N == 128) dl += shfl_xor(dl, 8);
       if (valid) {
-        const int hh = jc / N, n = jc % N;
+        const int hh = jc / N, n = jc - hh * N;
         const int b = mc / T, t = mc - b * T;
         const size_t hrow = ((size_t)b * H + hh) * T + t;
         st16(p.dO + hrow * N + n, pack8(dov));
@@ -143,17 +150,26 @@ __global__ __launch_bounds__(256) void dz_gate_bwd_kernel(DzParams p) {
         if (n == 0) p.delta[hrow] = dl;
       }
     }
-    __syncthreads();
   }
+}
+
+template <int NF>
+static void launch_dz_nf(const DzParams& p, int HN, hipStream_t s) {
+  const dim3 grid((p.M + TokShape<NF>::BT - 1) / TokShape<NF>::BT, (HN + NF - 1) / NF);
+  hipLaunchKernelGGL(dz_gate_bwd_kernel<NF>, grid, dim3(TokShape<NF>::NT), 0, s, p);
 }
 
 hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s) {
   const int HN = p.H * p.N;
-  const int G = ((p.M + 127) / 128) * ((HN + 255) / 256);
-  if (p.N == 64)
-    hipLaunchKernelGGL(dz_gate_bwd_kernel<64>, dim3(G), dim3(256), 0, s, p);
+  if (p.C % 32 != 0 || (p.N != 64 && p.N != 128)) return hipErrorInvalidValue;
+  if (HN == 512)
+    launch_dz_nf<512>(p, HN, s);
+  else if (HN == 768)
+    launch_dz_nf<768>(p, HN, s);
+  else if (HN == 1024)
+    launch_dz_nf<1024>(p, HN, s);
   else
-    hipLaunchKernelGGL(dz_gate_bwd_kernel<128>, dim3(G), dim3(256), 0, s, p);
+    launch_dz_nf<256>(p, HN, s);
   return hipGetLastError();
 }
 
