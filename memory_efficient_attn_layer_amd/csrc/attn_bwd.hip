@@ -118,8 +118,11 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // stay in registers as the B operands of
 //   S^T = K Q^T   and   dP^T = V dO^T      (A = K, V rows from LDS)
 // on v_mfma_f32_32x32x16_bf16. The query index sits on the lane, so the row
-// statistics lse and delta are per-lane registers and dS^T = P^T (dP^T -
-// delta) is already the B operand (k = key) of
+// statistics ride along as one more k-block of those products (stored q is
+// in log2 units): with -lse*log2e and -delta split into exact bf16 terms on
+// the query side and (1, 1, 1) selectors on the key side, the accumulators
+// come out as log2 P and dP - delta, and dS^T = P^T (dP^T - delta) is one
+// exp2 and one multiply per score, already the B operand (k = key) of
 //   dQ^T += K^T dS^T
 // whose A operand K^T is read from the row-major K tile with the transposing
 // ds_read_b64_tr_b16. Key tiles of 64 stream through LDS (global_load_lds,
@@ -137,8 +140,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   constexpr int LOADS = TILE / 8 / 256;
   constexpr int FP = N + 4;  // fp32 staging pitch
   constexpr int SM_LOOP = 4 * TILE * 2;  // bytes: [stage][K | V]
+  constexpr int SM_STAT = 4 * QB * 64 * 16;  // bytes: statistic k-blocks, [wave][qb][lane]
   constexpr int SM_OUT = 4 * QW * FP * 4;
-  constexpr int SMEM = SM_LOOP > SM_OUT ? SM_LOOP : SM_OUT;
+  constexpr int SMEM = SM_LOOP + SM_STAT > SM_OUT ? SM_LOOP + SM_STAT : SM_OUT;
   __shared__ __attribute__((aligned(16))) unsigned char smem_raw[SMEM];
   bf16_bits* smem = reinterpret_cast<bf16_bits*>(smem_raw);
 
@@ -158,10 +162,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   const bf16_bits* kg = p.k + head_off;
   const bf16_bits* vg = p.v + head_off;
 
-  // q^T and dO^T fragments (B operands) and the row statistics of the lane's
-  // query q0w + 32qb + c.
+  // q^T and dO^T fragments (B operands), and the statistic k-block of the
+  // lane's query q0w + 32qb + c: (-lse*log2e, -delta) in elements 0..5 of the
+  // lanes with h == 0 (zero in the others), kept in a wave-private LDS area
+  // the loop does not touch and matched by the selectors sel_s (S) and sel_d
+  // (dP). The selectors may be the same in every lane, which keeps them
+  // plain constants.
   bf16x8 qf[QB][KS], df[QB][KS];
-  float lse2[QB], dlt[QB];
+  u32x4* stat = reinterpret_cast<u32x4*>(smem_raw + SM_LOOP) + wave * QB * 64;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int t = min(q0w + 32 * qb + c, T - 1);
@@ -171,9 +179,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
       qf[qb][ks] = as_frag(ld16(p.q + off));
       df[qb][ks] = as_frag(ld16(p.dO + off));
     }
-    lse2[qb] = p.lse[(size_t)bh * T + t] * kLog2e;
-    dlt[qb] = p.delta[(size_t)bh * T + t];
+    const u32x4 sw = stat_pack(-p.lse[(size_t)bh * T + t] * kLog2e, -p.delta[(size_t)bh * T + t]);
+    stat[qb * 64 + lane] = h == 0 ? sw : u32x4{0u, 0u, 0u, 0u};
   }
+  const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
 
   auto issue_tile = [&](int j0, int stage) {
     bf16_bits* kt = smem + stage * 2 * TILE;
@@ -193,10 +202,19 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) dq[qb][db] = zero16();
 
+  // Lane-constant parts of the fragment addresses (elements): a row's
+  // swizzle depends on row & 15 only, so the step and k-step parts of an
+  // address are plain offsets.
   const int g16 = lane >> 4, i16 = lane & 15;
   const int tr_row = 4 * h + (i16 >> 2);
   const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
-  const float sl2e = p.sl2e;
+  int koff[KS], toff[2][DB];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = swz_off<CH>(c, 16 * ks + 8 * h);
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) toff[x][db] = swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col);
 
   // One 32-key step of every query block of this wave. MASK: the step
   // touches the causal diagonal or the end of the sequence.
@@ -205,9 +223,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
     bf16x8 kf[KS], vf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const int off = swz_off<CH>(st * 32 + c, 16 * ks + 8 * h);
-      kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + off));
-      vf[ks] = as_frag(*reinterpret_cast<const u32x4*>(vs_t + off));
+      kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + st * 32 * N + koff[ks]));
+      vf[ks] = as_frag(*reinterpret_cast<const u32x4*>(vs_t + st * 32 * N + koff[ks]));
     }
     bf16x8 sf[QB][2];
 #pragma unroll
@@ -217,7 +234,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
         sf[qb][0] = sf[qb][1] = as_frag(u32x4{0u, 0u, 0u, 0u});
         continue;
       }
-      f32x16 s = zero16(), dp = zero16();
+      const bf16x8 stf = as_frag(stat[qb * 64 + lane]);
+      f32x16 s = mfma32(sel_s, stf, zero16()), dp = mfma32(sel_d, stf, zero16());
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         s = mfma32(kf[ks], qf[qb][ks], s);
@@ -226,12 +244,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
       const int qq = qb0 + c;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float pv = fast_exp2(__builtin_fmaf(s[i], sl2e, -lse2[qb]));
+        float pv = fast_exp2(s[i]);
         if (MASK) {
           const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
           pv = (key > qq || key >= T) ? 0.f : pv;
         }
-        s[i] = pv * (dp[i] - dlt[qb]);
+        s[i] = pv * dp[i];
       }
 #pragma unroll
       for (int kst = 0; kst < 2; ++kst) {
@@ -240,14 +258,18 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
         for (int e = 0; e < 4; ++e) w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
         sf[qb][kst] = as_frag(w);
       }
+      // Keeps the next query block's S and dP accumulators from going live
+      // before this block's are consumed (they do not fit in registers
+      // together with the resident q, dO and dQ fragments).
+      if (QB > 1) __builtin_amdgcn_sched_barrier(0);
     }
     // dQ^T += K^T dS^T, two 16-key MFMA steps.
 #pragma unroll
     for (int kst = 0; kst < 2; ++kst) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const int r = st * 32 + 16 * kst + tr_row, col = 32 * db + tr_col;
-        const bf16x8 kt = frag_from2(lds_read_tr4(ks_t + swz_off<CH>(r, col)), lds_read_tr4(ks_t + swz_off<CH>(r + 8, col)));
+        const bf16_bits* kr = ks_t + (st * 32 + 16 * kst) * N;
+        const bf16x8 kt = frag_from2(lds_read_tr4(kr + toff[0][db]), lds_read_tr4(kr + toff[1][db]));
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           if (MASK && kb0 > q0w + 32 * qb + 31) continue;
@@ -308,8 +330,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 // consecutive keys (two waves fit per SIMD) whose K and V rows
 // stay in registers as the B operands of
 //   S  = Q K^T   and   dP = dO V^T        (A = Q, dO rows from LDS)
-// on v_mfma_f32_32x32x16_bf16. The key index sits on the lane, so P and
-// dS = P (dP - delta) are already the B operands (k = query) of
+// on v_mfma_f32_32x32x16_bf16, each with one more k-block that subtracts
+// the query statistics (stored q is in log2 units): -lse*log2e and -delta,
+// split into exact bf16 terms per query tile when its statistics are
+// published, on the query side, and (1, 1, 1) selectors on the key side. The
+// accumulators come out as log2 P and dP - delta. The key index sits on the
+// lane, so P and dS = P (dP - delta) are already the B operands (k = query) of
 //   dV^T += dO^T P   and   dK^T += Q^T dS
 // whose A operands dO^T, Q^T are read from the same row-major LDS tiles with
 // the transposing ds_read_b64_tr_b16. Query tiles of 64 stream through LDS
@@ -320,18 +346,21 @@ template <int N>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
   constexpr int KW = 32;                 // keys per wave
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
+  static_assert(KB == 1, "one 32-key block per wave");
   constexpr int BKV = 4 * KW;            // keys per workgroup
   constexpr int BQ = 64;                 // queries per LDS tile
   constexpr int CH = N / 8, KS = N / 16, DB = N / 32;
   constexpr int TILE = BQ * N;
   constexpr int LOADS = TILE / 8 / 256;
   constexpr int FP = N + 4;  // fp32 staging pitch
-  constexpr int SM_LOOP = 2 * 2 * TILE * 2 + 2 * 2 * BQ * 4;  // bytes
+  constexpr int SM_LOOP = 2 * 2 * TILE * 2 + 2 * (BQ + 1) * 16;  // bytes
   constexpr int SM_OUT = 4 * 32 * FP * 4;
   constexpr int SMEM = SM_LOOP > SM_OUT ? SM_LOOP : SM_OUT;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
   bf16_bits* tiles = reinterpret_cast<bf16_bits*>(smem);           // [stage][Q | dO]
-  float* stats = reinterpret_cast<float*>(smem + 2 * 2 * TILE * 2);  // [stage][lse*log2e | delta]
+  // [stage][query]: statistic k-block words of each query of the tile, then
+  // one zero block read by the lanes that hold k-elements 8..15.
+  u32x4* stats = reinterpret_cast<u32x4*>(smem + 2 * 2 * TILE * 2);
 
   const int T = p.T, BH = p.B * p.H;
   const int nkb = (T + BKV - 1) / BKV;
@@ -359,7 +388,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) 
     }
   }
 
-  float st_reg = 0.f;
+  float st_l = 0.f, st_d = 0.f;
+  if (tid < 2) stats[tid * (BQ + 1) + BQ] = u32x4{0u, 0u, 0u, 0u};
   auto issue_tile = [&](int q0, int stage) {
     bf16_bits* qt = tiles + stage * 2 * TILE;
 #pragma unroll
@@ -370,15 +400,16 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) 
       g2lds16(qg + off, qt + (u * 4 + wave) * 512);
       g2lds16(dg + off, qt + TILE + (u * 4 + wave) * 512);
     }
-    if (tid < 2 * BQ) {
-      const size_t t = (size_t)bh * T + min(q0 + (tid & (BQ - 1)), T - 1);
-      st_reg = tid < BQ ? p.lse[t] : p.delta[t];
+    if (tid < BQ) {
+      const size_t t = (size_t)bh * T + min(q0 + tid, T - 1);
+      st_l = p.lse[t];
+      st_d = p.delta[t];
     }
   };
-  // Called after wait_vmcnt0(): st_reg is consumed only once every load of
-  // the tile has landed, so no wait is placed inside the prefetch.
+  // Called after wait_vmcnt0(): st_l / st_d are consumed only once every load
+  // of the tile has landed, so no wait is placed inside the prefetch.
   auto publish_stats = [&](int stage) {
-    if (tid < 2 * BQ) stats[stage * 2 * BQ + tid] = tid < BQ ? st_reg * kLog2e : st_reg;
+    if (tid < BQ) stats[stage * (BQ + 1) + tid] = stat_pack(-st_l * kLog2e, -st_d);
   };
 
   f32x16 dv[KB][DB], dk[KB][DB];
@@ -387,9 +418,27 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) 
 #pragma unroll
     for (int db = 0; db < DB; ++db) dv[kb][db] = dk[kb][db] = zero16();
 
+  // Lane-constant parts of the fragment addresses (elements); a row's swizzle
+  // depends on row & 15 only.
   const int g16 = lane >> 4, i16 = lane & 15;
   const int tr_row = 4 * h + (i16 >> 2);
   const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+  // (N = 128 recomputes them per use: holding all of them there would spill.)
+  constexpr bool HOLD = N == 64;
+  int koff[HOLD ? KS : 1], toff[2][HOLD ? DB : 1];
+  auto kofs = [&](int ks) { return HOLD ? koff[HOLD ? ks : 0] : swz_off<CH>(c, 16 * ks + 8 * h); };
+  auto tofs = [&](int x, int db) { return HOLD ? toff[x][HOLD ? db : 0] : swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col); };
+  if (HOLD) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) koff[HOLD ? ks : 0] = swz_off<CH>(c, 16 * ks + 8 * h);
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) toff[x][HOLD ? db : 0] = swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col);
+  }
+  // Key-side selectors of the statistic k-block (the same in every lane: the
+  // query side is zero in the lanes holding k-elements 8..15).
+  const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
 
   const int nq = (T - k0 + BQ - 1) / BQ;
   issue_tile(k0, 0);
@@ -401,87 +450,99 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) 
     if (it + 1 < nq) issue_tile(q0 + BQ, (it + 1) & 1);
     const bf16_bits* qt = tiles + (it & 1) * 2 * TILE;
     const bf16_bits* dt = qt + TILE;
-    const float* ls = stats + (it & 1) * 2 * BQ;
-    const float* dls = ls + BQ;
-    // One 32-query step; DIAG steps mask key > query and query >= T with
-    // selects, the others run without any per-element test. Each variant is
-    // one basic block, so the scheduler can overlap the MFMAs of one key
-    // block with the exp/convert work of the other.
-    auto step = [&](int sub, auto diag_tag) {
-      constexpr bool DIAG = decltype(diag_tag)::value;
-      const int qs0 = q0 + 32 * sub;
+    const u32x4* sts = stats + (it & 1) * (BQ + 1);
+    // One 32-query step in three parts: S and dP (MFMA), P and dS (exp2,
+    // multiply, convert; DIAG steps also mask key > query and query >= T),
+    // then the dV and dK updates (MFMA).
+    struct Sub {
+      f32x16 s, dp;
+      bf16x8 pb[2], sb[2];
+    };
+    auto sdp = [&](int sub, Sub& u) {
       bf16x8 qa[KS], da[KS];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const int off = swz_off<CH>(32 * sub + c, 16 * ks + 8 * h);
-        qa[ks] = as_frag(*reinterpret_cast<const u32x4*>(qt + off));
-        da[ks] = as_frag(*reinterpret_cast<const u32x4*>(dt + off));
+        qa[ks] = as_frag(*reinterpret_cast<const u32x4*>(qt + 32 * sub * N + kofs(ks)));
+        da[ks] = as_frag(*reinterpret_cast<const u32x4*>(dt + 32 * sub * N + kofs(ks)));
       }
-      // Statistics of the queries held by accumulator register 4*r4 + e:
-      // query qs0 + 8*r4 + 4h + e.
-      f32x4 l4[4], d4[4];
+      // Statistic k-block of the lane's query row qs0 + c (zero for h == 1).
+      const bf16x8 sa = as_frag(sts[h == 0 ? 32 * sub + c : BQ]);
+      u.s = mfma32(sa, sel_s, zero16());
+      u.dp = mfma32(sa, sel_d, zero16());
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        l4[r4] = *reinterpret_cast<const f32x4*>(ls + 32 * sub + 8 * r4 + 4 * h);
-        d4[r4] = *reinterpret_cast<const f32x4*>(dls + 32 * sub + 8 * r4 + 4 * h);
+      for (int ks = 0; ks < KS; ++ks) {
+        u.s = mfma32(qa[ks], kf[0][ks], u.s);
+        u.dp = mfma32(da[ks], vf[0][ks], u.dp);
       }
-      bf16x8 pb[KB][2], sb[KB][2];
+    };
+    auto soft = [&](int sub, Sub& u, auto diag_tag) {
+      constexpr bool DIAG = decltype(diag_tag)::value;
+      const int qs0 = q0 + 32 * sub, key = kw0 + c;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          s = mfma32(qa[ks], kf[kb][ks], s);
-          dp = mfma32(da[ks], vf[kb][ks], dp);
+      for (int i = 0; i < 16; ++i) {
+        float pv = fast_exp2(u.s[i]);
+        if (DIAG) {
+          const int q = qs0 + 8 * (i >> 2) + 4 * h + (i & 3);
+          pv = (key > q || q >= T) ? 0.f : pv;
         }
-        const int key = kw0 + 32 * kb + c;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int r4 = i >> 2, e = i & 3;
-          float pv = fast_exp2(__builtin_fmaf(s[i], p.sl2e, -l4[r4][e]));
-          if (DIAG) {
-            const int q = qs0 + 8 * r4 + 4 * h + e;
-            pv = (key > q || q >= T) ? 0.f : pv;
-          }
-          s[i] = pv;
-          dp[i] = pv * (dp[i] - d4[r4][e]);
-        }
-#pragma unroll
-        for (int kst = 0; kst < 2; ++kst) {
-          u32x4 w, u;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
-            u[e] = pack2(dp[8 * kst + 2 * e], dp[8 * kst + 2 * e + 1]);
-          }
-          pb[kb][kst] = as_frag(w);
-          sb[kb][kst] = as_frag(u);
-        }
+        u.s[i] = pv;
+        u.dp[i] = pv * u.dp[i];
       }
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst) {
+        u32x4 w, v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          w[e] = pack2(u.s[8 * kst + 2 * e], u.s[8 * kst + 2 * e + 1]);
+          v[e] = pack2(u.dp[8 * kst + 2 * e], u.dp[8 * kst + 2 * e + 1]);
+        }
+        u.pb[kst] = as_frag(w);
+        u.sb[kst] = as_frag(v);
+      }
+    };
+    auto kv = [&](int sub, const Sub& u) {
 #pragma unroll
       for (int kst = 0; kst < 2; ++kst) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const int r = 32 * sub + 16 * kst + tr_row, col = 32 * db + tr_col;
-          const int o0 = swz_off<CH>(r, col), o1 = swz_off<CH>(r + 8, col);
+          const int rb = (32 * sub + 16 * kst) * N;
+          const int o0 = rb + tofs(0, db), o1 = rb + tofs(1, db);
           const bf16x8 dT = frag_from2(lds_read_tr4(dt + o0), lds_read_tr4(dt + o1));
           const bf16x8 qT = frag_from2(lds_read_tr4(qt + o0), lds_read_tr4(qt + o1));
-#pragma unroll
-          for (int kb = 0; kb < KB; ++kb) {
-            dv[kb][db] = mfma32(dT, pb[kb][kst], dv[kb][db]);
-            dk[kb][db] = mfma32(qT, sb[kb][kst], dk[kb][db]);
-          }
+          dv[0][db] = mfma32(dT, u.pb[kst], dv[0][db]);
+          dk[0][db] = mfma32(qT, u.sb[kst], dk[0][db]);
         }
       }
     };
+    if (N == 64 && it >= 2 && q0 + BQ <= T) {
+      // Both steps are below every wave's keys and inside the sequence (and
+      // N = 64: with N = 128 the two steps' operands do not fit). One
+      // basic block, fenced into phases so that each step's exp2 / convert
+      // work is issued among the other step's MFMAs:
+      //   S,dP(0) | S,dP(1) + P,dS(0) | dV,dK(0) + P,dS(1) | dV,dK(1)
+      Sub u0, u1;
+      sdp(0, u0);
+      __builtin_amdgcn_sched_barrier(0);
+      sdp(1, u1);
+      soft(0, u0, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+      kv(0, u0);
+      soft(1, u1, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+      kv(1, u1);
+    } else {
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int qs0 = q0 + 32 * sub;
-      if (qs0 + 31 < kw0 || qs0 >= T) continue;  // wave-uniform: nothing to add
-      if (qs0 < kw0 + KW - 1 || qs0 + 31 >= T)
-        step(sub, std::true_type{});
-      else
-        step(sub, std::false_type{});
+      for (int sub = 0; sub < 2; ++sub) {
+        const int qs0 = q0 + 32 * sub;
+        if (qs0 + 31 < kw0 || qs0 >= T) continue;  // wave-uniform: nothing to add
+        Sub u;
+        sdp(sub, u);
+        if (qs0 < kw0 + KW - 1 || qs0 + 31 >= T)
+          soft(sub, u, std::true_type{});
+        else
+          soft(sub, u, std::false_type{});
+        kv(sub, u);
+      }
     }
     wait_vmcnt0();
     if (it + 1 < nq) publish_stats((it + 1) & 1);
@@ -517,6 +578,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) 
 }
 
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
+  if (p.sl2e != 1.0f) return hipErrorInvalidValue;  // stored q must be in log2 units
   const int BQ = N == 64 ? 256 : 128;
   const int G = p.B * p.H * ((p.T + BQ - 1) / BQ);
   if (N == 64)
@@ -527,6 +589,7 @@ hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
 }
 
 hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s) {
+  if (p.sl2e != 1.0f) return hipErrorInvalidValue;  // stored q must be in log2 units
   const int BKV = 128;
   const int G = p.B * p.H * ((p.T + BKV - 1) / BKV);
   if (N == 64)

@@ -54,7 +54,7 @@ struct AttnBwdParams {
   float *df1, *df2;                         // (T, N) accumulators or null
   int B, H, T, ld_da;
   float scale;                              // softmax scale 1/sqrt(N)
-  float sl2e;                               // multiplies stored q . k into log2 units
+  float sl2e;                               // must be 1: stored q . k is in log2 units
   float qscale;                             // stored q = q * qscale
 };
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s);
