@@ -26,6 +26,8 @@
 // X X^T of each 16-token block, one extra MFMA per block and k-step on the x
 // fragments already in registers (the two waves sharing a token half split
 // the blocks).
+#include <type_traits>
+
 #include "kernels.h"
 #include "slab.cuh"
 
@@ -88,42 +90,60 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   const int nslab = ntl * nk;  // slabs this workgroup streams, over all its tiles
 
   const uint32_t lds0 = lds_addr(smem);
-  // Issues slab q of the stream: tile q / nk, k-slab q % nk, into stage q % NS.
-  auto issue = [&](int q) {
-    const int ti = q / nk, ks = q - ti * nk;
+  // Fetch cursor: slabs are issued in stream order, tile after tile. The
+  // per-tile part of every load address (row-group bases, uniform; lane
+  // offsets with the x rows clamped to the last token) is set when the
+  // cursor enters a tile, so issuing a slab only adds its k offset.
+  SlabPlan<BF, 4, BK> wplan;
+  slab_plan(wplan, wave, C, [](int, int i) { return i; });
+  SlabPlan<BT, 4, BK> xplan;
+  constexpr int NUW = SlabPlan<BF, 4, BK>::NU, NUX = SlabPlan<BT, 4, BK>::NU;
+  const bf16_bits* wbase[NUW];
+  const bf16_bits* xbase[NUX];
+  int iss_ti = 0, iss_ks = 0, iss_st = 0;
+  auto plan_tile = [&](int ti) {
     const ProjTile tl = proj_tile<N>(start + j0 + ti * nj, H);
-    const uint32_t lds = lds0 + (uint32_t)((q % NS) * STAGE) * 2u;
-    const int k0 = ks * BK;
     const bf16_bits* wseg[NSEG];
     if (NSEG == 4) {
+      // [q; v; k; g]: each wave's 128 features hold one rotary projection.
       wseg[0] = wq;
-      wseg[NSEG > 1 ? 1 : 0] = wk;
-      wseg[NSEG > 2 ? 2 : 0] = wv;
+      wseg[NSEG > 1 ? 1 : 0] = wv;
+      wseg[NSEG > 2 ? 2 : 0] = wk;
       wseg[NSEG > 3 ? 3 : 0] = wg;
     } else {
       wseg[0] = tl.f0 == 0 ? wq : wv;
       wseg[NSEG > 1 ? 1 : 0] = tl.f0 == 0 ? wk : wg;
     }
     // Stacked-weight rows: each 64-row load group lies inside one projection.
-    slab_issue<BF, 4, BK>(
-        lds, wave, C,
-        [&](int u) {
-          const int seg = (64 * u) / N;  // compile-time after unrolling
-          return wseg[seg] + (size_t)(tl.h * N + 64 * u - seg * N) * C + k0;
-        },
-        [](int, int i) { return i; });
-    // x rows, clamped to the last token.
-    slab_issue<BT, 4, BK>(
-        lds + BF * BK * 2, wave, C,
-        [&](int u) { return xg + (size_t)min(tl.m0 + 64 * u, M - 1) * C + k0; },
-        [&](int u, int i) { return min(tl.m0 + 64 * u + i, M - 1) - min(tl.m0 + 64 * u, M - 1); });
+#pragma unroll
+    for (int u = 0; u < NUW; ++u) {
+      const int seg = (64 * u) / N;  // compile-time after unrolling
+      wbase[u] = wseg[seg] + (size_t)(tl.h * N + 64 * u - seg * N) * C;
+    }
+#pragma unroll
+    for (int u = 0; u < NUX; ++u) xbase[u] = xg + (size_t)min(tl.m0 + 64 * u, M - 1) * C;
+    slab_plan(xplan, wave, C,
+              [&](int u, int i) { return min(tl.m0 + 64 * u + i, M - 1) - min(tl.m0 + 64 * u, M - 1); });
   };
+  auto issue_next = [&]() {
+    const uint32_t lds = lds0 + (uint32_t)(iss_st * STAGE) * 2u;
+    const int k0 = iss_ks * BK;
+    slab_issue_planned<BF, 4, BK>(lds, wave, wplan, [&](int u) { return wbase[u] + k0; });
+    slab_issue_planned<BT, 4, BK>(lds + BF * BK * 2, wave, xplan, [&](int u) { return xbase[u] + k0; });
+    iss_st = iss_st == NS - 1 ? 0 : iss_st + 1;
+    if (++iss_ks == nk) {
+      iss_ks = 0;
+      if (++iss_ti < ntl) plan_tile(iss_ti);
+    }
+  };
+  if (ntl > 0) plan_tile(0);
 
   f32x4 acc[FB][TB];
   f32x4 gram[GB];  // Gram blocks of token blocks GB*wf .. GB*wf+GB-1
 
-  if (nslab > 0) issue(0);
-  if (nslab > 1) issue(1);
+  if (nslab > 0) issue_next();
+  if (nslab > 1) issue_next();
+  int cmp_st = 0;  // stage of the slab being multiplied
   for (int ti = 0; ti < ntl; ++ti) {
     const ProjTile tl = proj_tile<N>(start + j0 + ti * nj, H);
 #pragma unroll
@@ -141,8 +161,9 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       else
         wait_vmcnt0();
       __syncthreads();
-      if (q + 2 < nslab) issue(q + 2);
-      const bf16_bits* As = smem + (q % NS) * STAGE;
+      if (q + 2 < nslab) issue_next();
+      const bf16_bits* As = smem + cmp_st * STAGE;
+      cmp_st = cmp_st == NS - 1 ? 0 : cmp_st + 1;
       const bf16_bits* Bs = As + BF * BK;
       bf16x8 af[FB], bfr[TB];
 #pragma unroll
@@ -162,6 +183,34 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       }
     }
 
+    // Rotary table rows of the wave's tokens are fetched ahead of their use
+    // and before the stores that precede it: a load waits for every memory
+    // operation issued before it (vmcnt counts stores too), so a table row
+    // fetched after a block's stores would wait for their acknowledgement.
+    const int m0 = tl.m0, h = tl.h;
+    const int b0 = m0 / T, t0 = m0 - b0 * T;
+    const bool tile_whole = m0 + BT <= M && t0 + BT <= T;
+    const bool has_rot = N == 64 || tl.f0 == 0;  // the wave holds q or k
+    auto tab_row = [&](int tb) {
+      const int m = m0 + wt * (TB * 16) + tb * 16 + c16;
+      return tile_whole ? t0 + (m - m0) : (m < M ? m - (m / T) * T : 0);
+    };
+    // N = 64: one slot of table rows, filled for block 0 at the start of the
+    // epilogue and refilled, feature block by feature block, for block tb + 1
+    // as block tb consumes it. N = 128 (twice the rows) reads each feature
+    // block's rows just before use.
+    constexpr bool PREF = N == 64;
+    f32x4 tab1[PREF ? GF : 1], tab2[PREF ? GF : 1];
+    auto tab_at = [&](const float* f, int tb, int j) {
+      return *reinterpret_cast<const f32x4*>(f + (size_t)tab_row(tb) * N + 16 * j + 4 * g);
+    };
+    auto load_tab_j = [&](int tb, int j) {
+      if (PREF) {
+        tab1[PREF ? j : 0] = tab_at(p.f1, tb, j);
+        tab2[PREF ? j : 0] = tab_at(p.f2, tb, j);
+      }
+    };
+
     // Diagonal of each Gram block: token c16 of the block sits in lane
     // (g = c16 / 4, c16), register c16 % 4.
 #pragma unroll
@@ -176,10 +225,12 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
 
     // Row coordinates. A tile inside one sequence (the usual case: T a
     // multiple of 128) needs no per-row division or bounds checks.
-    const int m0 = tl.m0, h = tl.h;
     const float inv_c = 1.0f / (float)C, inv_n = 1.0f / (float)N, eps = p.eps;
-    const int b0 = m0 / T, t0 = m0 - b0 * T;
-    const bool whole = m0 + BT <= M && t0 + BT <= T;
+    // Everything below is instantiated twice: for a whole tile (one sequence,
+    // inside M: no per-row division or bounds test) and for the rest.
+    float nmax = 0.f;  // largest squared row norm of the wave's rotary projection
+    auto epilogue = [&](auto whole_tag) {
+    constexpr bool whole = decltype(whole_tag)::value;
     int trow[TB], brow[TB];
     bool ok[TB];
     float rx[TB];
@@ -199,6 +250,11 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       if (p.rx != nullptr && h == 0 && tl.f0 == 0 && wf == 0 && g == 0 && ok[tb]) p.rx[m] = rx[tb];
     }
 
+    if (PREF && has_rot) {
+#pragma unroll
+      for (int j = 0; j < GF; ++j) load_tab_j(0, j);
+    }
+
     // Output staging: the stage of the tile's last slab is free until the
     // next tile's third slab is issued (after that tile's first barrier).
     // Each wave owns a 16-token x (NPW * N) block of it, rows of N + 8
@@ -206,125 +262,136 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     // drained as 16-byte row chunks, so every store covers whole rows.
     constexpr int SP = N + 8;
     bf16_bits* stg = smem + ((ti * nk + nk - 1) % NS) * STAGE + wave * (NPW * 16 * SP);
-    const int pj0 = (tl.f0 + wf * 128) / N;  // first projection of this wave (wave-uniform)
+    // Projection (0 q, 1 k, 2 v, 3 g) of the wave's gi-th N-feature block,
+    // wave-uniform. For N = 64 the stacked rows are [q; v; k; g], so every
+    // wave owns one rotary projection and one plain one and the epilogue work
+    // is the same in all four waves; for N = 128 a tile is (q, k) or (v, g).
+    auto proj_of = [&](int gi) { return N == 64 ? (gi == 0 ? wf : 2 + wf) : (tl.f0 == 0 ? 0 : 2) + wf; };
     constexpr int CPR = N / 8;               // 16-byte chunks per output row
     // Drains the staged block of projection gi for token block tb into
     // dstp + b * bstride + t * tstride.
     auto drain = [&](int gi, int tb, bf16_bits* dstp, size_t bstride, size_t tstride) {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+      bf16_bits* tile0 = dstp + (size_t)b0 * bstride + (size_t)t0 * tstride;  // whole tiles
 #pragma unroll
       for (int it = 0; it < 16 * CPR / 64; ++it) {
         const int id = lane + 64 * it, row = id / CPR, ch = id % CPR;
         const int tl_row = wt * (TB * 16) + tb * 16 + row;
         const u32x4 val = *reinterpret_cast<const u32x4*>(stg + (gi * 16 + row) * SP + ch * 8);
-        if (whole || m0 + tl_row < M) {
-          const int m = m0 + tl_row;
-          const int bb = whole ? b0 : m / T, tt = whole ? t0 + tl_row : m - (m / T) * T;
+        if (whole) {
+          st16(tile0 + (uint32_t)(tl_row * (int)tstride + ch * 8), val);
+        } else if (m0 + tl_row < M) {
+          const int m = m0 + tl_row, bb = m / T, tt = m - bb * T;
           st16(dstp + (size_t)bb * bstride + (size_t)tt * tstride + ch * 8, val);
         }
       }
     };
-    if (pj0 < 2) {
-      // Head RMSNorm over N (fast_triton_attn.py:102-106) of a = rx * acc:
-      // 1/rms(a) = rsqrt(rx^2 mean(acc^2) + eps), one scale rx / rms(a) per
-      // row. The rotary (:132-141) then acts on the fp32 normalised values:
-      // out[n] = qh[n] f1[t,n] + qh[n^1] f2[t,n]; q rows are stored times
-      // qscale. The largest squared row norm of each projection is recorded
-      // for the attention's logit bound.
-      float nmax[NPW];
+    // Head RMSNorm over N (fast_triton_attn.py:102-106) of a = rx * acc:
+    // 1/rms(a) = rsqrt(rx^2 mean(acc^2) + eps), one scale rx / rms(a) per
+    // row. The rotary (:132-141) then acts on the fp32 normalised values:
+    // out[n] = qh[n] f1[t,n] + qh[n^1] f2[t,n]; q rows are stored times
+    // qscale. The largest squared row norm is recorded for the attention's
+    // logit bound. `next` >= 0 names the block whose table rows refill the
+    // slot.
+    auto rot_block = [&](int tb, int gi, int next) {
+      // Fenced, so the refill loads stay behind the reads of the slot.
+      __builtin_amdgcn_sched_barrier(0);
+      const int pj = proj_of(gi);
+      const int t = ok[tb] ? trow[tb] : 0;
+      float ss = 0.f;
 #pragma unroll
-      for (int gi = 0; gi < NPW; ++gi) nmax[gi] = 0.f;
+      for (int j = 0; j < GF; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ss += acc[gi * GF + j][tb][r] * acc[gi * GF + j][tb][r];
+      ss += shfl_xor(ss, 16);
+      ss += shfl_xor(ss, 32);
+      const float rr = rsqrtf(rx[tb] * rx[tb] * ss * inv_n + eps);
+      const float sc = rx[tb] * rr * (pj == 0 ? p.qscale : 1.0f);  // folded into the table rows
+      if (ok[tb] && g == 0) {
+        float* rstat = pj == 0 ? p.rq : p.rk;
+        if (rstat != nullptr) rstat[((size_t)brow[tb] * H + h) * T + t] = rr;
+      }
+      float nrm = 0.f;
+#pragma unroll
+      for (int j = 0; j < GF; ++j) {
+        const int n = 16 * j + 4 * g;
+        const f32x4 a1 = (PREF ? tab1[PREF ? j : 0] : tab_at(p.f1, tb, j)) * sc;
+        const f32x4 a2 = (PREF ? tab2[PREF ? j : 0] : tab_at(p.f2, tb, j)) * sc;
+        if (next >= 0) load_tab_j(next, j);
+        const f32x4& a = acc[gi * GF + j][tb];
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          o[r] = a[r] * a1[r] + a[r ^ 1] * a2[r];
+          nrm += o[r] * o[r];
+        }
+        *reinterpret_cast<u32x2*>(stg + (gi * 16 + c16) * SP + n) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+      }
+      nrm += shfl_xor(nrm, 16);
+      nrm += shfl_xor(nrm, 32);
+      nmax = fmaxf(nmax, nrm);
+    };
+    // v = rx acc; g = sigmoid(rx acc) = 1 / (1 + exp2(-log2(e) rx acc)).
+    auto plain_block = [&](int tb, int gi) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int pj = proj_of(gi);
+      const float kx = pj == 2 ? rx[tb] : -kLog2e * rx[tb];
+#pragma unroll
+      for (int j = 0; j < GF; ++j) {
+        const f32x4& a = acc[gi * GF + j][tb];
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = pj == 2 ? a[r] * kx : __builtin_amdgcn_rcpf(1.0f + fast_exp2(a[r] * kx));
+        *reinterpret_cast<u32x2*>(stg + (gi * 16 + c16) * SP + 16 * j + 4 * g) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+      }
+    };
+    auto drain_pj = [&](int gi, int tb) {
+      const int pj = proj_of(gi);
+      if (pj < 2)
+        drain(gi, tb, (pj == 0 ? p.q : p.k) + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
+      else if (pj == 2)
+        drain(gi, tb, p.v + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
+      else
+        drain(gi, tb, p.sig + (size_t)h * N, (size_t)T * HN, (size_t)HN);
+    };
+    if (N == 64) {
+      // The plain projection (v or g) of every block first, while the table
+      // rows of blocks 0 and 1 arrive; then the rotary one, each block
+      // refilling its slot with the rows of block tb + 2.
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) {
-        float sc[NPW], rr[NPW], nrm[NPW];
-#pragma unroll
-        for (int gi = 0; gi < NPW; ++gi) {
-          float s = 0.f;
-#pragma unroll
-          for (int j = 0; j < GF; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) s += acc[gi * GF + j][tb][r] * acc[gi * GF + j][tb][r];
-          s += shfl_xor(s, 16);
-          s += shfl_xor(s, 32);
-          rr[gi] = rsqrtf(rx[tb] * rx[tb] * s * inv_n + eps);
-          sc[gi] = rx[tb] * rr[gi] * (pj0 + gi == 0 ? p.qscale : 1.0f);
-          nrm[gi] = 0.f;
-        }
-        const int t = ok[tb] ? trow[tb] : 0;
-        if (ok[tb] && g == 0) {
-          const size_t hrow = ((size_t)brow[tb] * H + h) * T + t;
-#pragma unroll
-          for (int gi = 0; gi < NPW; ++gi) {
-            float* rstat = pj0 + gi == 0 ? p.rq : p.rk;
-            if (rstat != nullptr) rstat[hrow] = rr[gi];
-          }
-        }
-        const float* f1r = p.f1 + (size_t)t * N;
-        const float* f2r = p.f2 + (size_t)t * N;
-#pragma unroll
-        for (int j = 0; j < GF; ++j) {
-          const int n = 16 * j + 4 * g;
-          const f32x4 a1 = *reinterpret_cast<const f32x4*>(f1r + n);
-          const f32x4 a2 = *reinterpret_cast<const f32x4*>(f2r + n);
-#pragma unroll
-          for (int gi = 0; gi < NPW; ++gi) {
-            const f32x4& a = acc[gi * GF + j][tb];
-            float o[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              o[r] = (a[r] * a1[r] + a[r ^ 1] * a2[r]) * sc[gi];
-              nrm[gi] += o[r] * o[r];
-            }
-            *reinterpret_cast<u32x2*>(stg + (gi * 16 + c16) * SP + n) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
-          }
-        }
-#pragma unroll
-        for (int gi = 0; gi < NPW; ++gi) {
-          float v = nrm[gi];
-          v += shfl_xor(v, 16);
-          v += shfl_xor(v, 32);
-          nmax[gi] = fmaxf(nmax[gi], v);
-        }
-#pragma unroll
-        for (int gi = 0; gi < NPW; ++gi)
-          drain(gi, tb, (pj0 + gi == 0 ? p.q : p.k) + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
+        plain_block(tb, 1);
+        drain_pj(1, tb);
       }
-      if (p.qk_norm2 != nullptr) {
 #pragma unroll
-        for (int gi = 0; gi < NPW; ++gi) {
-          float v = nmax[gi];
-          v = fmaxf(v, xor1(v));
-          v = fmaxf(v, xor2(v));
-          v = fmaxf(v, shfl_xor(v, 4));
-          v = fmaxf(v, shfl_xor(v, 8));
-          // Non-negative floats order like their bit patterns.
-          if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(p.qk_norm2) + (pj0 + gi), __float_as_uint(v));
-        }
+      for (int tb = 0; tb < TB; ++tb) {
+        rot_block(tb, 0, tb + 1 < TB ? tb + 1 : -1);
+        drain_pj(0, tb);
       }
     } else {
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) {
-#pragma unroll
-        for (int gi = 0; gi < NPW; ++gi) {
-          const bool is_v = pj0 + gi == 2;
-#pragma unroll
-          for (int j = 0; j < GF; ++j) {
-            const f32x4& a = acc[gi * GF + j][tb];
-            float o[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[r] = is_v ? a[r] * rx[tb] : fast_sigmoid(a[r] * rx[tb]);
-            *reinterpret_cast<u32x2*>(stg + (gi * 16 + c16) * SP + 16 * j + 4 * g) =
-                u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
-          }
-        }
-#pragma unroll
-        for (int gi = 0; gi < NPW; ++gi) {
-          if (pj0 + gi == 2)
-            drain(gi, tb, p.v + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
-          else
-            drain(gi, tb, p.sig + (size_t)h * N, (size_t)T * HN, (size_t)HN);
-        }
+        if (has_rot)
+          rot_block(tb, 0, -1);
+        else
+          plain_block(tb, 0);
+        drain_pj(0, tb);
       }
+    }
+    };
+    if (tile_whole)
+      epilogue(std::true_type{});
+    else
+      epilogue(std::false_type{});
+    const int pjr = N == 64 ? wf : (tl.f0 == 0 ? 0 : 2) + wf;  // the rotary projection, if any
+    if (p.qk_norm2 != nullptr && pjr < 2) {
+      float v = nmax;
+      v = fmaxf(v, xor1(v));
+      v = fmaxf(v, xor2(v));
+      v = fmaxf(v, shfl_xor(v, 4));
+      v = fmaxf(v, shfl_xor(v, 8));
+      // Non-negative floats order like their bit patterns.
+      if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(p.qk_norm2) + pjr, __float_as_uint(v));
     }
   }
 }

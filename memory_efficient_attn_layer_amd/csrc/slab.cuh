@@ -49,6 +49,40 @@ __device__ __forceinline__ void slab_issue(uint32_t lds, int wave, int stride, B
   }
 }
 
+// The per-lane half of slab_issue, for callers that fetch many slabs with
+// the same rows: byte offset of this lane's 16-byte chunk for each of its
+// load instructions (row_of and the swizzle do not depend on k). Slabs are
+// then issued with slab_issue_planned, which only adds a per-slab base.
+template <int R, int NW, int KS>
+struct SlabPlan {
+  static constexpr int CH = KS / 8, RPI = 64 / CH, NI = R / RPI, NU = (NI + NW - 1) / NW;
+  uint32_t voff[NU];
+};
+template <int R, int NW, int KS, class RowOf>
+__device__ __forceinline__ void slab_plan(SlabPlan<R, NW, KS>& pl, int wave, int stride, RowOf row_of) {
+  using P = SlabPlan<R, NW, KS>;
+  static_assert(R % P::RPI == 0, "slab rows");
+  const int lane = threadIdx.x & 63;
+  const int i = wave * P::RPI + lane / P::CH;
+#pragma unroll
+  for (int u = 0; u < P::NU; ++u) {
+    const int ins = u * NW + wave;
+    const int row = ins * P::RPI + lane / P::CH;
+    const int chunk = (lane % P::CH) ^ slab_swz<KS>(row);
+    pl.voff[u] = (uint32_t)(row_of(u, i) * stride + chunk * 8) * 2u;
+  }
+}
+template <int R, int NW, int KS, class Base>
+__device__ __forceinline__ void slab_issue_planned(uint32_t lds, int wave, const SlabPlan<R, NW, KS>& pl, Base base) {
+  using P = SlabPlan<R, NW, KS>;
+#pragma unroll
+  for (int u = 0; u < P::NU; ++u) {
+    const int ins = u * NW + wave;
+    if (P::NI % NW != 0 && ins >= P::NI) break;  // wave-uniform: partial last round
+    g2lds16_s(base(u), pl.voff[u], lds + (uint32_t)ins * 1024u);
+  }
+}
+
 // 16-byte read of chunk `chunk` of slab row `row`.
 template <int KS>
 __device__ __forceinline__ u32x4 slab_read(const bf16_bits* lds, int row, int chunk) {
