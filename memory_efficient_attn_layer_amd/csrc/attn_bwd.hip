@@ -327,7 +327,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 // dK, dV
 //
 // One workgroup = one (batch, head) and BKV = 4*KW keys; wave w owns KW = 32
-// consecutive keys (two waves fit per SIMD) whose K and V rows
+// consecutive keys (two waves per SIMD for N = 64; for N = 128 one wave per
+// SIMD, whose 512 registers hold the operands without spilling) whose K and V rows
 // stay in registers as the B operands of
 //   S  = Q K^T   and   dP = dO V^T        (A = Q, dO rows from LDS)
 // on v_mfma_f32_32x32x16_bf16, each with one more k-block that subtracts
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 // block's first key (causal).
 // ---------------------------------------------------------------------------
 template <int N>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
   constexpr int KW = 32;                 // keys per wave
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
   static_assert(KB == 1, "one 32-key block per wave");
@@ -514,9 +515,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnBwdParams p) 
         }
       }
     };
-    if (N == 64 && it >= 2 && q0 + BQ <= T) {
-      // Both steps are below every wave's keys and inside the sequence (and
-      // N = 64: with N = 128 the two steps' operands do not fit). One
+    if (it >= 2 && q0 + BQ <= T) {
+      // Both steps are below every wave's keys and inside the sequence. One
       // basic block, fenced into phases so that each step's exp2 / convert
       // work is issued among the other step's MFMAs:
       //   S,dP(0) | S,dP(1) + P,dS(0) | dV,dK(0) + P,dS(1) | dV,dK(1)
