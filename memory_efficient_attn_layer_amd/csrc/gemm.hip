@@ -64,12 +64,10 @@ static void launch_oproj_nf(const OprojParams& p, hipStream_t s) {
 
 hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s) {
   if (p.C % 256 != 0 || p.HN % 32 != 0) return hipErrorInvalidValue;
-  if (p.C == 256)
-    launch_oproj_nf<256>(p, s);
-  else if (p.C == 768)
+  // Feature groups of 512 (or 256): a group of 1024 would shrink the token
+  // block to 64 and re-read all of Wo from L2 for every 64 tokens.
+  if (p.C == 768)
     launch_oproj_nf<768>(p, s);
-  else if (p.C == 1024)
-    launch_oproj_nf<1024>(p, s);
   else if (p.C % 512 == 0)
     launch_oproj_nf<512>(p, s);
   else
@@ -162,12 +160,11 @@ static void launch_dz_nf(const DzParams& p, int HN, hipStream_t s) {
 hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s) {
   const int HN = p.H * p.N;
   if (p.C % 32 != 0 || (p.N != 64 && p.N != 128)) return hipErrorInvalidValue;
-  if (HN == 512)
-    launch_dz_nf<512>(p, HN, s);
-  else if (HN == 768)
+  // Feature groups of 512 where HN allows (see launch_gate_oproj).
+  if (HN == 768)
     launch_dz_nf<768>(p, HN, s);
-  else if (HN == 1024)
-    launch_dz_nf<1024>(p, HN, s);
+  else if (HN % 512 == 0)
+    launch_dz_nf<512>(p, HN, s);
   else
     launch_dz_nf<256>(p, HN, s);
   return hipGetLastError();
