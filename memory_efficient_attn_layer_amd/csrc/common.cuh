@@ -75,7 +75,15 @@ __device__ __forceinline__ void g2lds16(const void* gsrc, bf16_bits* lds_wave_ba
 // per-lane byte offset (saddr form), into the LDS byte address lds (also
 // wave-uniform). Saves the per-lane 64-bit address arithmetic.
 __device__ __forceinline__ void g2lds16_s(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+  // The base and the LDS address must sit in SGPRs; readfirstlane states
+  // that they are uniform where the compiler cannot prove it (free where it
+  // can).
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  const uint64_t u = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"((const void*)(uintptr_t)u),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
 }
 // LDS byte address of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)((lds_void*)p); }
