@@ -29,6 +29,10 @@ STAGE_CASES = [
     ("cfg3-b1-t512", _w("c3", 1, 512, 1024, 8, 128), None),
     ("ragged-b3-t77", _w("r", 3, 77, 256, 2, 64), None),
     ("yarn4-b1-t300", _w("y", 1, 300, 512, 4, 64, 4.0, 128), None),
+    # Forward-only widths (C > 1024): the output projection in 256- and
+    # 512-feature groups.
+    ("c1280-h4-b1-t64", _w("c1280", 1, 64, 1280, 4, 64), None),
+    ("c2048-h8-n128-b1-t64", _w("c2048", 1, 64, 2048, 8, 128), None),
 ]
 
 
@@ -95,6 +99,9 @@ BLOCK_CASES = [
     ("c-ne-hn-b2-t160", _w("chn", 2, 160, 512, 4, 64), None),
     ("c768-b1-t100", _w("c768", 1, 100, 768, 4, 64), None),
     ("yarn8-b2-t300-n128", _w("y8", 2, 300, 256, 2, 128, 8.0, 64), None),
+    # H*N not a multiple of 256: the dZ kernel's last feature group is partial.
+    ("h5-hn320-b1-t150", _w("h5", 1, 150, 256, 5, 64), None),
+    ("h3-hn192-b2-t70", _w("h3", 2, 70, 512, 3, 64), None),
 ]
 
 
