@@ -6,8 +6,9 @@
 // variants (:181-332) when rx/rq/rk are requested.
 //
 // The product is computed transposed, D^T = W x^T: the A operand is a slice
-// of the stacked weights [Wq_h; Wk_h; Wv_h; Wg_h] of one head h (features),
-// the B operand a tile of x rows (tokens). In the 16x16 accumulator layout a
+// of the stacked weights of one head h (features; [Wq_h; Wv_h; Wk_h; Wg_h]
+// for N = 64, [Wq_h; Wk_h] and [Wv_h; Wg_h] tiles for N = 128), the B
+// operand a tile of x rows (tokens). In the 16x16 accumulator layout a
 // lane then holds one token and 4 consecutive features, so the head RMSNorm
 // is an in-lane sum plus two lane exchanges, both members of every rotary
 // pair (n, n^1) sit in one lane, and results leave as 8-byte stores.
@@ -16,9 +17,9 @@
 // LDS ring filled by direct global->LDS loads, two slabs ahead, continuously
 // across the tiles a workgroup walks (one barrier per slab). Four waves of
 // 128 features x 64 tokens (32 accumulators of 16x16): for N = 64 a wave owns
-// two projections of its tokens, (q, k) or (v, g), so the rotary table rows
-// of its tokens are fetched once for both q and k. Two workgroups share a CU,
-// so one's epilogue overlaps the other's products.
+// one rotary projection (q or k) and one plain one (v or g) of its tokens, so
+// the epilogue work is the same in every wave. Two workgroups share a CU, so
+// one's epilogue can overlap the other's products.
 //
 // The input RMSNorm is never materialised: diag(1/rms(x)) commutes with the
 // GEMM, so the row scale multiplies the fp32 accumulator. The row sums of
