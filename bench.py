@@ -13,6 +13,8 @@ timed region), peak HBM, and the CPU baseline (the fp32 oracle on a bounded
 batch slice on the host cores). Progress goes to stderr.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--compare-eager] [--no-cpu-baseline]
+    python bench.py --workload 2|3       # the same line for another fwd+bwd workload
+    python bench.py --workload 4         # forward-only (prefill) workload: fwd tokens/s, no CPU leg
     python bench.py --copy-calibration   # a plain 256 MiB device copy, for HBM counter scaling
 """
 from __future__ import annotations
@@ -27,6 +29,12 @@ import time
 from pathlib import Path
 
 METRIC = "fwd+bwd tokens/s & peak mem, attn block bf16 B64 T4096 C512 H8 N64"
+
+
+def metric_of(w) -> str:
+    """The metric string of a workload (the north-star one for workload 1)."""
+    kind = "fwd+bwd" if w.backward else "fwd (prefill, no grad)"
+    return f"{kind} tokens/s & peak mem, attn block bf16 B{w.B} T{w.T} C{w.C} H{w.H} N{w.N}"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 ROOT = Path(__file__).resolve().parent
@@ -175,7 +183,8 @@ def main():
 
     w = WORKLOADS[args.workload]
     if not w.backward:
-        raise SystemExit(f"workload {args.workload} is forward-only; bench.py measures fwd+bwd")
+        forward_bench(args, w)
+        return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"workload {w.name}; generating inputs")
@@ -218,9 +227,11 @@ def main():
     dom = max((k for k in prof if k in work), key=lambda k: prof[k][1])
     avg_s = prof[dom][1] / prof[dom][0] * 1e-3
     achieved = work[dom]["flops"] / avg_s / 1e12
+    # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE runs,
+    # which cover the north-star workload only.
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
-    if tfile.exists():
+    if w.wid == 1 and tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get(dom)
         except (ValueError, OSError):
@@ -264,7 +275,7 @@ def main():
         log(f"cpu: {cpu['value']:.1f} tokens/s on {cpu['cores']} cores")
 
     out = {
-        "metric": METRIC,
+        "metric": metric_of(w),
         "value": round(tokens / sec, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -284,6 +295,81 @@ def main():
         "attention": attention,
         "kernels": kernels,
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def roofline_of(prof, work):
+    """Roofline entry of the kernel with the largest total time."""
+    dom = max((k for k in prof if k in work), key=lambda k: prof[k][1])
+    avg_s = prof[dom][1] / prof[dom][0] * 1e-3
+    achieved = work[dom]["flops"] / avg_s / 1e12
+    return {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
+
+
+def forward_bench(args, w):
+    """Forward-only (prefill) workload: the inference forward under no_grad
+    (no saved O / lse), timed like the training step. The fp32 CPU oracle
+    cannot run a sequence of this length in bounded time, so there is no CPU
+    leg."""
+    import torch
+
+    from memory_efficient_attn_layer_amd import _lib
+    from memory_efficient_attn_layer_amd.attention import FusedAttentionFunction
+    from memory_efficient_attn_layer_amd.synthetic import make_inputs
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"workload {w.name} (forward only); generating inputs")
+    inp = make_inputs(w, device=dev)
+    args_in = [inp[n] for n in ("x", "wq", "wk", "wv", "wg", "wo", "f1", "f2")]
+    sync = torch.cuda.synchronize
+
+    def step():
+        with torch.no_grad():
+            return FusedAttentionFunction.apply(*args_in, w.H, w.N, 1e-6)
+
+    log("warm-up")
+    for _ in range(max(1, args.warmup)):
+        step()
+    sync()
+    peak = peak_of(step, sync)
+    _lib.profile_enable(True)
+    sec = measure(step, args.steps, 0, sync)
+    _lib.profile_enable(False)
+    prof = _lib.profile_read()
+    tokens = w.B * w.T
+    log(f"{sec * 1e3:.3f} ms/step, {tokens / sec / 1e6:.3f} M tokens/s, peak {peak / 2**20:.1f} MiB")
+    work = kernel_work(w)
+    kernels = {}
+    for name, (cnt, tot) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        avg = tot / cnt
+        ent = {"launches_per_step": cnt / args.steps, "avg_ms": round(avg, 4), "share": round(tot / (sec * 1e3 * args.steps), 4)}
+        if name in work:
+            ent["tflops"] = round(work[name]["flops"] / (avg * 1e-3) / 1e12, 2)
+        kernels[name] = ent
+        log(f"  {name:15s} {avg:8.4f} ms x{cnt / args.steps:.0f}  {ent.get('tflops', '-')} TFLOP/s")
+    out = {
+        "metric": metric_of(w),
+        "value": round(tokens / sec, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": w.name, "B": w.B, "T": w.T, "C": w.C, "H": w.H, "N": w.N,
+                   "tokens_per_step": tokens, "parallelism": "single-gpu"},
+        "peak_hbm": {"fused_bytes": int(peak)},
+        "block_tflops": round(w.flops_fwd() / sec / 1e12, 2),
+        "roofline": roofline_of(prof, work),
+        "kernels": kernels,
+        "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
 
