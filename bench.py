@@ -15,6 +15,8 @@ batch slice on the host cores). Progress goes to stderr.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--compare-eager] [--no-cpu-baseline]
     python bench.py --workload 2|3       # the same line for another fwd+bwd workload
     python bench.py --workload 4         # forward-only (prefill) workload: fwd tokens/s, no CPU leg
+    python bench.py --workload W --decode [--context L]
+                                         # KV-cache decode steps at context L (default T - 1)
     python bench.py --copy-calibration   # a plain 256 MiB device copy, for HBM counter scaling
 """
 from __future__ import annotations
@@ -157,6 +159,9 @@ def main():
     ap.add_argument("--compare-eager", action="store_true", help="also time the eager SDPA path on the GPU")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--decode", action="store_true",
+                    help="time KV-cache decode steps (one token per sequence) instead of fwd+bwd")
+    ap.add_argument("--context", type=int, default=None, help="decode: cached tokens per sequence (default T - 1)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 256 MiB five times (reference for HBM byte counters)")
     args = ap.parse_args()
@@ -182,6 +187,9 @@ def main():
     from memory_efficient_attn_layer_amd.synthetic import WORKLOADS, make_inputs
 
     w = WORKLOADS[args.workload]
+    if args.decode:
+        decode_bench(args, w)
+        return
     if not w.backward:
         forward_bench(args, w)
         return
@@ -368,6 +376,87 @@ def forward_bench(args, w):
         "peak_hbm": {"fused_bytes": int(peak)},
         "block_tflops": round(w.flops_fwd() / sec / 1e12, 2),
         "roofline": roofline_of(prof, work),
+        "kernels": kernels,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def decode_bench(args, w):
+    """KV-cache decode: a prompt of L tokens per sequence is prefilled, then
+    every timed step decodes one token per sequence at position L (the same
+    position each step, so every step reads the same L + 1 cache rows). The
+    step is bound by HBM: the roofline is the decode attention's cache bytes
+    per launch over its live average duration, against 8 TB/s."""
+    import torch
+
+    from memory_efficient_attn_layer_amd import _lib
+    from memory_efficient_attn_layer_amd.decode import KVCache, decode_step, prefill
+    from memory_efficient_attn_layer_amd.synthetic import make_inputs
+
+    L = w.T - 1 if args.context is None else int(args.context)
+    if not 0 <= L < w.T:
+        raise SystemExit(f"--context must be in [0, {w.T - 1}] for workload {w.wid}")
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"workload {w.name}: decode at context {L}; generating inputs")
+    inp = make_inputs(w, device=dev)
+    H, N, B, C = w.H, w.N, w.B, w.C
+    wts = [inp[n] for n in ("wq", "wk", "wv", "wg", "wo")]
+    f1, f2 = inp["f1"].float(), inp["f2"].float()
+    cache = KVCache.empty(B, H, N, w.T, dev)
+    if L > 0:
+        prefill(inp["x"][:, :L], *wts, f1, f2, H, N, cache)
+    xt = inp["x"][:, min(L, w.T - 1)].contiguous()
+    pos = torch.full((B,), L, dtype=torch.int32, device=dev)
+    del inp
+    sync = torch.cuda.synchronize
+
+    def step():
+        return decode_step(xt, *wts, f1, f2, H, N, pos, cache)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    sync()
+    peak = peak_of(step, sync)
+    steps = max(args.steps, 50)
+    _lib.profile_enable(True)
+    sec = measure(step, steps, 0, sync)
+    _lib.profile_enable(False)
+    prof = _lib.profile_read()
+    HN = H * N
+    kv_bytes = 2.0 * B * H * (L + 1) * N * 2
+    w_bytes = 2.0 * 5 * HN * C
+    kernels = {}
+    for name, (cnt, tot) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        kernels[name] = {"launches_per_step": cnt / steps, "avg_ms": round(tot / cnt, 5),
+                         "share": round(tot / (sec * 1e3 * steps), 4)}
+        log(f"  {name:20s} {tot / cnt * 1e3:9.2f} us")
+    dec_ms = prof["attn_decode"][1] / prof["attn_decode"][0]
+    achieved = kv_bytes / (dec_ms * 1e-3) / 1e9
+    log(f"{sec * 1e6:.1f} us/step, {B / sec:.0f} tokens/s; cache read {achieved:.0f} GB/s")
+    out = {
+        "metric": f"decode tokens/s (one token per sequence per step) at context {L}, attn block bf16 "
+                  f"B{B} C{C} H{H} N{N}",
+        "value": round(B / sec, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": w.name, "B": B, "context": L, "C": C, "H": H, "N": N,
+                   "cache_bytes_read_per_step": int(kv_bytes), "weight_bytes_per_step": int(w_bytes),
+                   "parallelism": "single-gpu"},
+        "step_hbm_gbs": round((kv_bytes + w_bytes) / sec / 1e9, 1),
+        "peak_hbm": {"step_bytes": int(peak)},
+        "roofline": {"kernel": "attn_decode", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": None},
         "kernels": kernels,
         "cpu_baseline": None,
     }

@@ -118,6 +118,53 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq,
             size_t ws_bytes, void* stream);
 
 /*
+ * Prefill of a KV cache: the inference forward of a whole prompt (mea_fwd
+ * with o_save = lse_save = NULL, same workspace) that also copies the
+ * prompt's k and v rows, exactly as the attention consumed them, into rows
+ * 0..T-1 of the caller's caches. No counterpart in the reference, which
+ * trains only; it is the prompt half of the decode step below.
+ *
+ *   x .. f2, y           as in mea_fwd (d->T = prompt length)
+ *   k_cache, v_cache     (B, H, cache_T, N) bf16; k rows are RMS-normalised
+ *                        and rotated, v rows plain; T <= cache_T <= T_max
+ */
+int mea_prefill(const mea_desc* d, const void* x, const void* wq,
+                const void* wk, const void* wv, const void* wg,
+                const void* wo, const float* f1, const float* f2, void* y,
+                void* k_cache, void* v_cache, int64_t cache_T, void* ws,
+                size_t ws_bytes, void* stream);
+
+/*
+ * Workspace bytes needed by mea_decode (d->T = cache capacity). Returns 0
+ * when the descriptor is invalid.
+ */
+size_t mea_decode_workspace_bytes(const mea_desc* d);
+
+/*
+ * KV-cache decode step: one new token per sequence. No counterpart in the
+ * reference (training only); the block math is that of mea_fwd for the last
+ * row of a causal sequence. The new token of sequence b sits at position
+ * pos[b]: it reads rotary row pos[b], its k and v are written to cache row
+ * pos[b], and it attends to cache rows 0..pos[b] (its own included).
+ *
+ *   d->T              cache capacity Tc (<= d->T_max)
+ *   x                 (B, C) bf16            the new tokens
+ *   wq .. wo, f1, f2  as in mea_fwd
+ *   pos               (B) int32, device      0 <= pos[b] < Tc; values outside
+ *                                            are clamped to that range
+ *   k_cache, v_cache  (B, H, Tc, N) bf16     rows 0..pos[b]-1 hold the
+ *                                            earlier tokens (mea_prefill or
+ *                                            earlier steps); row pos[b] is
+ *                                            written
+ *   y                 (B, C) bf16            out
+ */
+int mea_decode(const mea_desc* d, const void* x, const void* wq,
+               const void* wk, const void* wv, const void* wg, const void* wo,
+               const float* f1, const float* f2, const int32_t* pos,
+               void* k_cache, void* v_cache, void* y, void* ws,
+               size_t ws_bytes, void* stream);
+
+/*
  * Stage: input RMSNorm + q/k/v/g projection + per-head q/k RMSNorm + rotary +
  * sigmoid. Replaces rms_norm_kernel(_recompute) and
  * fused_qkvg_norm_rope_kernel(_recompute) (fast_triton_attn.py:12-144,

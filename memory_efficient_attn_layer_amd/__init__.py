@@ -5,6 +5,7 @@ xTimeCrystal/memory_efficient_attn_layer (fast_triton_attn.py:373-697), backed
 by hand-written HIP kernels in libmea.so (C ABI: include/mea.h).
 """
 from .attention import FusedAttentionFunction, fused_attn
+from .decode import KVCache, decode_step, prefill
 from .module import CausalSoftmaxAttention
 from .yarn import Yarn, rotary_tables, swap_even_odd
 
@@ -12,6 +13,9 @@ __all__ = [
     "FusedAttentionFunction",
     "fused_attn",
     "CausalSoftmaxAttention",
+    "KVCache",
+    "prefill",
+    "decode_step",
     "Yarn",
     "rotary_tables",
     "swap_even_odd",

@@ -46,6 +46,9 @@ EXPORTS = {
         ctypes.c_int,
         [_desc] + [_vp] * 7 + [_fp, _fp, _vp, _fp] + [_vp] * 6 + [_fp, _fp, _vp, ctypes.c_size_t, _vp],
     ),
+    "mea_prefill": (ctypes.c_int, [_desc] + [_vp] * 6 + [_fp, _fp, _vp, _vp, _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _vp]),
+    "mea_decode_workspace_bytes": (ctypes.c_size_t, [_desc]),
+    "mea_decode": (ctypes.c_int, [_desc] + [_vp] * 6 + [_fp, _fp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "mea_qkvg_proj": (ctypes.c_int, [_desc] + [_vp] * 5 + [_fp, _fp] + [_vp] * 4 + [_fp, _fp, _fp, _vp]),
     "mea_attn_fwd": (ctypes.c_int, [_desc, _vp, _vp, _vp, _vp, _fp, _vp]),
     "mea_gate_oproj": (ctypes.c_int, [_desc, _vp, _vp, _vp, _vp, _vp]),

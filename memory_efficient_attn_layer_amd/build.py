@@ -23,7 +23,7 @@ OBJ = PKG / "_build"
 LIB = PKG / "libmea.so"
 INCLUDE = PKG.parent / "include"
 
-SOURCES = ["api.hip", "proj.hip", "attn_fwd.hip", "attn_bwd.hip", "gemm.hip"]
+SOURCES = ["api.hip", "proj.hip", "attn_fwd.hip", "attn_bwd.hip", "gemm.hip", "decode.hip"]
 
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32.
 HIPCC_FLAGS = [

@@ -91,11 +91,13 @@ T* at(void* ws, size_t off) {
 // ---- kernel timing diagnostics -------------------------------------------
 enum KernelId {
   K_QKVG_PROJ, K_ATTN_FWD, K_GATE_OPROJ, K_TRANSPOSE, K_ZERO, K_DZ_GATE_BWD,
-  K_ATTN_BWD_DQ, K_ATTN_BWD_DKDV, K_DW_PARTIAL, K_DW_REDUCE, K_DX, K_COUNT
+  K_ATTN_BWD_DQ, K_ATTN_BWD_DKDV, K_DW_PARTIAL, K_DW_REDUCE, K_DX,
+  K_KV_APPEND, K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_COUNT
 };
 const char* const kKernelNames[K_COUNT] = {
     "qkvg_proj", "attn_fwd", "gate_oproj", "transpose", "zero_f32", "dz_gate_bwd",
-    "attn_bwd_dq", "attn_bwd_dkdv", "dw_partial", "dw_reduce", "dx"};
+    "attn_bwd_dq", "attn_bwd_dkdv", "dw_partial", "dw_reduce", "dx",
+    "kv_append", "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj"};
 
 struct ProfRec {
   int kernel;
@@ -407,6 +409,152 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   dxp.C = C;
   dxp.HN = HN;
   MEA_TRY(timed(K_DX, s, [&] { return mea::launch_dx(dxp, s); }));
+  return MEA_OK;
+}
+
+int mea_prefill(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+                const void* wo, const float* f1, const float* f2, void* y, void* k_cache, void* v_cache,
+                int64_t cache_T, void* ws, size_t ws_bytes, void* stream) {
+  int rc = validate(d, MEA_PASS_FWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({k_cache, v_cache});
+  if (rc != MEA_OK) return rc;
+  if (cache_T < d->T || cache_T > d->T_max) return MEA_ERR_SHAPE;
+  rc = mea_fwd(d, x, wq, wk, wv, wg, wo, f1, f2, y, nullptr, nullptr, ws, ws_bytes, stream);
+  if (rc != MEA_OK) return rc;
+  // The prompt's k / v rows (as the attention consumed them) into rows
+  // 0 .. T-1 of every (b, h) block of the caches.
+  const Layout L = make_layout(*d, MEA_PASS_FWD);
+  const size_t row = (size_t)(d->T * d->N * 2), pitch = (size_t)(cache_T * d->N * 2);
+  const size_t rows = (size_t)(d->B * d->H);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MEA_TRY(hipMemcpy2DAsync(k_cache, pitch, at<void>(ws, L.k), row, row, rows, hipMemcpyDeviceToDevice, s));
+  MEA_TRY(hipMemcpy2DAsync(v_cache, pitch, at<void>(ws, L.v), row, row, rows, hipMemcpyDeviceToDevice, s));
+  return MEA_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Decode workspace: the raw products [a_q|a_k|a_v|a_g] (B x 4HN fp32), the
+// new token's q, k, v, sigmoid(g) and attention output (B x H*N bf16 each)
+// and the split partials.
+struct DecLayout {
+  size_t a, q, k, v, sig, o, part, total;
+  int S, chunk;
+};
+
+DecLayout make_dec_layout(const mea_desc& d) {
+  DecLayout L = {};
+  mea::decode_splits((int)d.B, (int)d.H, (int)d.T, &L.S, &L.chunk);
+  const size_t row = (size_t)(d.B * d.H * d.N) * 2;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes); return o; };
+  L.a = take(row * 2 * 4);
+  L.q = take(row);
+  L.k = take(row);
+  L.v = take(row);
+  L.sig = take(row);
+  L.o = take(row);
+  L.part = take((size_t)(d.B * d.H) * L.S * (size_t)(d.N + 4) * 4);
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mea_decode_workspace_bytes(const mea_desc* d) {
+  if (validate(d, MEA_PASS_FWD) != MEA_OK) return 0;
+  return make_dec_layout(*d).total;
+}
+
+int mea_decode(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+               const void* wo, const float* f1, const float* f2, const int32_t* pos, void* k_cache, void* v_cache,
+               void* y, void* ws, size_t ws_bytes, void* stream) {
+  int rc = validate(d, MEA_PASS_FWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({x, wq, wk, wv, wg, wo, f1, f2, k_cache, v_cache, y, ws});
+  if (rc != MEA_OK) return rc;
+  if (pos == nullptr) return MEA_ERR_NULL;
+  if (((uintptr_t)pos & 3u) != 0) return MEA_ERR_ALIGN;
+  const DecLayout L = make_dec_layout(*d);
+  if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
+  const int N = (int)d->N, B = (int)d->B, C = (int)d->C, HN = (int)(d->H * d->N);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* a = at<float>(ws, L.a);
+  bf16_bits* q = at<bf16_bits>(ws, L.q);
+  bf16_bits* k = at<bf16_bits>(ws, L.k);
+  bf16_bits* v = at<bf16_bits>(ws, L.v);
+  bf16_bits* sig = at<bf16_bits>(ws, L.sig);
+  bf16_bits* o = at<bf16_bits>(ws, L.o);
+  // Projections of the B new tokens (a few rows: every weight row is read
+  // once over a wide grid), then their epilogue at rotary rows pos[b].
+  mea::SkinnyParams sp;
+  sp.A0 = static_cast<const bf16_bits*>(x);
+  sp.A1 = nullptr;
+  sp.W[0] = static_cast<const bf16_bits*>(wq);
+  sp.W[1] = static_cast<const bf16_bits*>(wk);
+  sp.W[2] = static_cast<const bf16_bits*>(wv);
+  sp.W[3] = static_cast<const bf16_bits*>(wg);
+  sp.out = a;
+  sp.M = B;
+  sp.K = C;
+  sp.F = HN;
+  sp.nw = 4;
+  sp.ldo = 4 * HN;
+  sp.out_bf16 = 0;
+  MEA_TRY(timed(K_SKINNY_GEMM, s, [&] { return mea::launch_skinny_gemm(sp, s); }));
+  mea::DecodeProjParams pp;
+  pp.a = a;
+  pp.x = static_cast<const bf16_bits*>(x);
+  pp.f1 = f1;
+  pp.f2 = f2;
+  pp.pos = pos;
+  pp.q = q;
+  pp.k = k;
+  pp.v = v;
+  pp.sig = sig;
+  pp.B = B;
+  pp.C = C;
+  pp.H = (int)d->H;
+  pp.t_max = (int)d->T_max;
+  pp.eps = d->eps;
+  pp.qscale = q_log2_scale(N);
+  MEA_TRY(timed(K_DECODE_PROJ, s, [&] { return mea::launch_decode_proj_epilogue(pp, N, s); }));
+  mea::DecodeParams dp;
+  dp.q = q;
+  dp.k_new = k;
+  dp.v_new = v;
+  dp.k_cache = static_cast<bf16_bits*>(k_cache);
+  dp.v_cache = static_cast<bf16_bits*>(v_cache);
+  dp.pos = pos;
+  dp.part = at<float>(ws, L.part);
+  dp.o = o;
+  dp.B = (int)d->B;
+  dp.H = (int)d->H;
+  dp.Tc = (int)d->T;
+  dp.S = L.S;
+  dp.chunk = L.chunk;
+  MEA_TRY(timed(K_KV_APPEND, s, [&] { return mea::launch_kv_append(dp, N, s); }));
+  MEA_TRY(timed(K_ATTN_DECODE, s, [&] { return mea::launch_attn_decode(dp, N, s); }));
+  MEA_TRY(timed(K_DECODE_COMBINE, s, [&] { return mea::launch_attn_decode_combine(dp, N, s); }));
+  // y = (O * sigmoid(g)) W_o^T for the B tokens.
+  mea::SkinnyParams op;
+  op.A0 = o;
+  op.A1 = sig;
+  op.W[0] = static_cast<const bf16_bits*>(wo);
+  op.W[1] = op.W[2] = op.W[3] = nullptr;
+  op.out = y;
+  op.M = B;
+  op.K = HN;
+  op.F = C;
+  op.nw = 1;
+  op.ldo = C;
+  op.out_bf16 = 1;
+  MEA_TRY(timed(K_SKINNY_GEMM, s, [&] { return mea::launch_skinny_gemm(op, s); }));
   return MEA_OK;
 }
 

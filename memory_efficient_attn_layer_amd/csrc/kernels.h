@@ -132,4 +132,52 @@ hipError_t launch_transpose(const bf16_bits* in, int rows, int cols, int ld_in, 
 // Fills n floats with zero (a kernel, so it is safe inside captured graphs).
 hipError_t launch_zero_f32(float* p, size_t n, hipStream_t s);
 
+// KV-cache decode step: one new token per sequence at position pos[b]
+// attends to cache rows 0 .. pos[b] (its own k / v included).
+struct DecodeParams {
+  const bf16_bits* q;                       // (B, H, N) stored q (log2 units)
+  const bf16_bits *k_new, *v_new;           // (B, H, N) the new token's k, v
+  bf16_bits *k_cache, *v_cache;             // (B, H, Tc, N)
+  const int* pos;                           // (B); clamped to [0, Tc - 1]
+  float* part;                              // (B*H, S, N + 4): o[N], m, l per split
+  bf16_bits* o;                             // (B, H*N) attention output
+  int B, H, Tc;
+  int S;                                    // key splits per (b, h), a multiple of 4
+  int chunk;                                // keys per split, a multiple of 64
+};
+// Splits and keys per split for a cache of Tc rows (host side).
+void decode_splits(int B, int H, int Tc, int* S, int* chunk);
+
+// Few-token products of the decode step: out[t][f] = sum_k A[t][k] W[f][k]
+// for t < M (M small), with A = A0 * A1 elementwise when A1 is given; up to
+// four weight matrices (W[z], F rows each) side by side in one launch, their
+// outputs at column z * F of out. fp32 or bf16 output.
+struct SkinnyParams {
+  const bf16_bits *A0, *A1;                 // (M, K), row stride K; A1 may be null
+  const bf16_bits* W[4];                    // (F, K) each
+  void* out;                                // (M, ldo)
+  int M, K, F, nw, ldo;
+  int out_bf16;
+};
+hipError_t launch_skinny_gemm(const SkinnyParams& p, hipStream_t s);
+
+// Epilogue of the decode projection for the new token of every sequence:
+// from a = [a_q | a_k | a_v | a_g] (B, 4HN) fp32 (products with the raw x)
+// and x, the input RMSNorm scale, per-head RMSNorm of q and k, rotary at
+// row pos[b] (clamped to t_max - 1), q times qscale, v, sigmoid(g).
+struct DecodeProjParams {
+  const float* a;                           // (B, 4HN)
+  const bf16_bits* x;                       // (B, C)
+  const float *f1, *f2;                     // (t_max, N)
+  const int* pos;                           // (B)
+  bf16_bits *q, *k, *v;                     // (B, H, N)
+  bf16_bits* sig;                           // (B, HN)
+  int B, C, H, t_max;
+  float eps, qscale;
+};
+hipError_t launch_decode_proj_epilogue(const DecodeProjParams& p, int N, hipStream_t s);
+hipError_t launch_kv_append(const DecodeParams& p, int N, hipStream_t s);
+hipError_t launch_attn_decode(const DecodeParams& p, int N, hipStream_t s);
+hipError_t launch_attn_decode_combine(const DecodeParams& p, int N, hipStream_t s);
+
 }  // namespace mea

@@ -1,0 +1,127 @@
+"""KV-cache inference for the block: ``prefill`` a prompt into a cache, then
+``decode_step`` one new token per sequence.
+
+The reference trains only and has no decode path; these run the same block
+math (README.md:42-64) through ``mea_prefill`` / ``mea_decode`` of libmea.so.
+The cache holds, per (batch, head), the k rows exactly as the attention uses
+them (RMS-normalised over N and rotated) and the plain v rows, bf16, in a
+``(B, H, capacity, N)`` layout. Sequence b's new token sits at position
+``pos[b]``: it reads rotary row ``pos[b]``, its k / v are written to cache row
+``pos[b]``, and it attends to rows ``0 .. pos[b]``, so sequences of a batch may
+have different lengths.
+
+Rotary tables are read in fp32 rows ``0 .. capacity-1``; pass fp32 tables to
+avoid a conversion per step.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .attention import MAX_C_FORWARD, SUPPORTED_HEAD_DIMS, _validate
+
+
+@dataclass
+class KVCache:
+    """Per-layer cache: ``k`` and ``v`` of shape (B, H, capacity, N), bf16."""
+
+    k: torch.Tensor
+    v: torch.Tensor
+
+    @classmethod
+    def empty(cls, B: int, H: int, N: int, capacity: int, device) -> "KVCache":
+        shape = (B, H, capacity, N)
+        return cls(torch.zeros(shape, device=device, dtype=torch.bfloat16),
+                   torch.zeros(shape, device=device, dtype=torch.bfloat16))
+
+    @property
+    def capacity(self) -> int:
+        return self.k.shape[2]
+
+    def check(self, B: int, H: int, N: int, device) -> None:
+        for name, t in (("k", self.k), ("v", self.v)):
+            if tuple(t.shape) != (B, H, self.capacity, N):
+                raise ValueError(f"cache.{name} has shape {tuple(t.shape)}, expected {(B, H, self.capacity, N)}")
+            if t.dtype != torch.bfloat16 or not t.is_contiguous():
+                raise ValueError(f"cache.{name} must be a contiguous bfloat16 tensor")
+            if t.device != device:
+                raise ValueError(f"cache.{name} is on {t.device}, x is on {device}")
+
+
+def _tables(factor1, factor2, rows: int):
+    if factor1.shape[0] < rows:
+        raise ValueError(f"rotary tables have {factor1.shape[0]} rows, fewer than the cache capacity {rows}")
+    return factor1[:rows].float().contiguous(), factor2[:rows].float().contiguous()
+
+
+def prefill(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H: int, N: int,
+            cache: KVCache, eps: float = 1e-6) -> torch.Tensor:
+    """Inference forward of a prompt ``x`` (B, T, C); writes its k / v rows to
+    rows 0..T-1 of ``cache`` and returns y (B, T, C)."""
+    H, N, eps = int(H), int(N), float(eps)
+    weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
+    _validate(x, weights, factor1, factor2, H, N, eps, False)
+    B, T, C = x.shape
+    cache.check(B, H, N, x.device)
+    Tc = cache.capacity
+    if Tc < T:
+        raise ValueError(f"cache capacity {Tc} is smaller than the prompt length {T}")
+    lib = _lib.load()
+    dev = x.device
+    xc = x.contiguous()
+    wc = [w.contiguous() for w in weights]
+    f1, f2 = _tables(factor1, factor2, Tc)
+    d = _lib.desc(B, T, C, H, N, Tc, eps)
+    y = torch.empty((B, T, C), device=dev, dtype=torch.bfloat16)
+    ws_bytes = lib.mea_workspace_bytes(d, _lib.MEA_PASS_FWD)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        rc = lib.mea_prefill(d, xc.data_ptr(), *[w.data_ptr() for w in wc], f1.data_ptr(), f2.data_ptr(),
+                             y.data_ptr(), cache.k.data_ptr(), cache.v.data_ptr(), Tc, ws.data_ptr(), ws_bytes,
+                             _lib.stream_of(dev))
+    _lib.check(rc, "mea_prefill")
+    return y
+
+
+def decode_step(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H: int, N: int,
+                pos, cache: KVCache, eps: float = 1e-6) -> torch.Tensor:
+    """One new token per sequence: ``x`` (B, C) or (B, 1, C) at positions
+    ``pos`` (B,) (an int32 device tensor or a sequence of ints, each in
+    [0, capacity)); returns y with the shape of ``x``."""
+    H, N, eps = int(H), int(N), float(eps)
+    weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
+    squeeze = x.dim() == 2
+    x3 = x.unsqueeze(1) if squeeze else x
+    if x3.dim() != 3 or x3.shape[1] != 1:
+        raise ValueError(f"x must be (B, C) or (B, 1, C), got {tuple(x.shape)}")
+    _validate(x3, weights, factor1, factor2, H, N, eps, False)
+    B, _, C = x3.shape
+    dev = x3.device
+    cache.check(B, H, N, dev)
+    Tc = cache.capacity
+    if not isinstance(pos, torch.Tensor):
+        pos = torch.tensor(list(pos), dtype=torch.int32, device=dev)
+    if pos.shape != (B,) or pos.dtype != torch.int32 or pos.device != dev:
+        raise ValueError(f"pos must be an int32 tensor of shape ({B},) on {dev}")
+    lib = _lib.load()
+    xc = x3.contiguous()
+    wc = [w.contiguous() for w in weights]
+    posc = pos.contiguous()
+    f1, f2 = _tables(factor1, factor2, Tc)
+    d = _lib.desc(B, Tc, C, H, N, Tc, eps)
+    y = torch.empty((B, 1, C), device=dev, dtype=torch.bfloat16)
+    ws_bytes = lib.mea_decode_workspace_bytes(d)
+    if ws_bytes == 0:
+        raise ValueError("unsupported decode shape")
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        rc = lib.mea_decode(d, xc.data_ptr(), *[w.data_ptr() for w in wc], f1.data_ptr(), f2.data_ptr(),
+                            posc.data_ptr(), cache.k.data_ptr(), cache.v.data_ptr(), y.data_ptr(), ws.data_ptr(),
+                            ws_bytes, _lib.stream_of(dev))
+    _lib.check(rc, "mea_decode")
+    return y[:, 0] if squeeze else y
+
+
+__all__ = ["KVCache", "prefill", "decode_step", "SUPPORTED_HEAD_DIMS", "MAX_C_FORWARD"]

@@ -7,6 +7,7 @@ import torch
 from torch import nn
 
 from .attention import fused_attn
+from .decode import KVCache, decode_step, prefill
 
 
 class CausalSoftmaxAttention(nn.Module):
@@ -31,3 +32,21 @@ class CausalSoftmaxAttention(nn.Module):
     def forward(self, x, yarn):
         return fused_attn(x, self.q_proj, self.k_proj, self.v_proj, self.g_proj, self.o_proj, yarn,
                           self.num_heads, self.head_dim)
+
+    # Inference with a KV cache (no counterpart in the reference, which
+    # trains only): the prompt fills the cache, then one token per sequence
+    # per step.
+    def new_cache(self, batch: int, capacity: int, device=None) -> KVCache:
+        dev = self.q_proj.weight.device if device is None else device
+        return KVCache.empty(batch, self.num_heads, self.head_dim, capacity, dev)
+
+    def prefill(self, x, yarn, cache: KVCache):
+        return prefill(x, *self._weights(), yarn.factor1, yarn.factor2, self.num_heads, self.head_dim, cache)
+
+    def decode(self, x, yarn, pos, cache: KVCache):
+        return decode_step(x, *self._weights(), yarn.factor1, yarn.factor2, self.num_heads, self.head_dim,
+                           pos, cache)
+
+    def _weights(self):
+        return (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.g_proj.weight,
+                self.o_proj.weight)

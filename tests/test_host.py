@@ -112,6 +112,38 @@ def test_pointer_and_workspace_validation(lib):
     assert lib.mea_bwd(ctypes.byref(d2), *bargs, 1 << 40, None) == _header_enum("MEA_ERR_MODEL_DIM")
 
 
+def test_decode_and_prefill_validation(lib):
+    fake = 1 << 20  # aligned, never dereferenced: validation fails first
+    d = _d(T=512, T_max=512)  # decode: T is the cache capacity
+    assert lib.mea_decode_workspace_bytes(None) == 0
+    assert lib.mea_decode_workspace_bytes(ctypes.byref(_d(N=96))) == 0
+    need = lib.mea_decode_workspace_bytes(ctypes.byref(d))
+    assert need >= 5 * 2 * 4 * 64 * 2  # q, k, v, sigmoid(g), O of the B new tokens
+    # decode pointers: x wq wk wv wg wo f1 f2 pos k_cache v_cache y ws
+    dargs = [fake] * 13
+    assert lib.mea_decode(ctypes.byref(d), *dargs, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
+    no_pos = list(dargs)
+    no_pos[8] = None
+    assert lib.mea_decode(ctypes.byref(d), *no_pos, need, None) == _header_enum("MEA_ERR_NULL")
+    odd_pos = list(dargs)
+    odd_pos[8] = fake + 2
+    assert lib.mea_decode(ctypes.byref(d), *odd_pos, need, None) == _header_enum("MEA_ERR_ALIGN")
+    no_cache = list(dargs)
+    no_cache[9] = None
+    assert lib.mea_decode(ctypes.byref(d), *no_cache, need, None) == _header_enum("MEA_ERR_NULL")
+    # Cache capacity beyond the rotary tables.
+    assert lib.mea_decode(ctypes.byref(_d(T=600, T_max=512)), *dargs, need, None) == _header_enum("MEA_ERR_SHAPE")
+    # prefill pointers: x wq wk wv wg wo f1 f2 y k_cache v_cache, cache_T, ws
+    pd = _d(T=64, T_max=128)
+    pargs = [fake] * 11
+    assert lib.mea_prefill(ctypes.byref(pd), *pargs, 32, fake, 1 << 40, None) == _header_enum("MEA_ERR_SHAPE")
+    assert lib.mea_prefill(ctypes.byref(pd), *pargs, 256, fake, 1 << 40, None) == _header_enum("MEA_ERR_SHAPE")
+    assert lib.mea_prefill(ctypes.byref(pd), *pargs, 128, fake, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
+    p_no_cache = list(pargs)
+    p_no_cache[10] = None
+    assert lib.mea_prefill(ctypes.byref(pd), *p_no_cache, 128, fake, 1 << 40, None) == _header_enum("MEA_ERR_NULL")
+
+
 def _cpu_args(B=1, T=8, C=256, H=4, N=64, dtype=torch.bfloat16):
     HN = H * N
     x = torch.randn(B, T, C, dtype=dtype)
