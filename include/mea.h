@@ -118,6 +118,37 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq,
             size_t ws_bytes, void* stream);
 
 /*
+ * Packed variable-length sequences (the cum_seq slots of the reference's
+ * aten flash call, fast_triton_attn.py:431-432, which it leaves unused):
+ * mea_fwd / mea_bwd over nseq sequences stored back to back, attention
+ * causal inside each sequence and rotary rows counted from each sequence's
+ * first token.
+ *
+ *   d->B                 1; d->T = total tokens = cu_seqlens[nseq]
+ *   cu_seqlens           (nseq + 1) int32, device: 0 = cu[0] <= cu[1] <= ...
+ *   max_len              >= every cu[s+1] - cu[s]; d->T_max >= max_len
+ *   x, y, dy, dx         (T, C) bf16;  o_save (T, H*N);  lse_save (H, T)
+ *   df1, df2             rows 0 .. max_len-1 written
+ *   workspace            mea_workspace_bytes(d, pass) with d->T_max raised to
+ *                        d->T if smaller (the sizes depend on B, T, C, H, N)
+ * Everything else as in mea_fwd / mea_bwd.
+ */
+int mea_fwd_varlen(const mea_desc* d, const int32_t* cu_seqlens, int32_t nseq,
+                   int32_t max_len, const void* x, const void* wq,
+                   const void* wk, const void* wv, const void* wg,
+                   const void* wo, const float* f1, const float* f2, void* y,
+                   void* o_save, float* lse_save, void* ws, size_t ws_bytes,
+                   void* stream);
+int mea_bwd_varlen(const mea_desc* d, const int32_t* cu_seqlens, int32_t nseq,
+                   int32_t max_len, const void* dy, const void* x,
+                   const void* wq, const void* wk, const void* wv,
+                   const void* wg, const void* wo, const float* f1,
+                   const float* f2, const void* o_save, const float* lse_save,
+                   void* dx, void* dwq, void* dwk, void* dwv, void* dwg,
+                   void* dwo, float* df1, float* df2, void* ws,
+                   size_t ws_bytes, void* stream);
+
+/*
  * Prefill of a KV cache: the inference forward of a whole prompt (mea_fwd
  * with o_save = lse_save = NULL, same workspace) that also copies the
  * prompt's k and v rows, exactly as the attention consumed them, into rows

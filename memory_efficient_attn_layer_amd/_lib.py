@@ -46,6 +46,15 @@ EXPORTS = {
         ctypes.c_int,
         [_desc] + [_vp] * 7 + [_fp, _fp, _vp, _fp] + [_vp] * 6 + [_fp, _fp, _vp, ctypes.c_size_t, _vp],
     ),
+    "mea_fwd_varlen": (
+        ctypes.c_int,
+        [_desc, _vp, ctypes.c_int32, ctypes.c_int32] + [_vp] * 6 + [_fp, _fp, _vp, _vp, _fp, _vp, ctypes.c_size_t, _vp],
+    ),
+    "mea_bwd_varlen": (
+        ctypes.c_int,
+        [_desc, _vp, ctypes.c_int32, ctypes.c_int32] + [_vp] * 7 + [_fp, _fp, _vp, _fp] + [_vp] * 6
+        + [_fp, _fp, _vp, ctypes.c_size_t, _vp],
+    ),
     "mea_prefill": (ctypes.c_int, [_desc] + [_vp] * 6 + [_fp, _fp, _vp, _vp, _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _vp]),
     "mea_decode_workspace_bytes": (ctypes.c_size_t, [_desc]),
     "mea_decode": (ctypes.c_int, [_desc] + [_vp] * 6 + [_fp, _fp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),

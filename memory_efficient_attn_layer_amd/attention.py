@@ -167,3 +167,120 @@ def fused_attn(x, q_proj, k_proj, v_proj, g_proj, o_proj, yarn_module, H, N, eps
         N,
         eps,
     )
+
+
+class FusedAttentionVarlenFunction(torch.autograd.Function):
+    """The block over packed variable-length sequences: x is (total, C), the
+    sequences lie back to back with offsets cu_seqlens (nseq + 1, int32, on
+    the device); attention is causal inside each sequence and the rotary row
+    of a token is its position in its sequence. The reference's aten call
+    carries the (unused) cum_seq slots for this (fast_triton_attn.py:431-432).
+    Gradients as in FusedAttentionFunction; table gradients cover rows
+    0 .. max_len - 1."""
+
+    @staticmethod
+    def forward(ctx, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, cu_seqlens, max_len, H,
+                N, eps):
+        H, N, eps, max_len = int(H), int(N), float(eps), int(max_len)
+        weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
+        if not isinstance(x, torch.Tensor) or x.dim() != 2:
+            raise ValueError("x must be a (total_tokens, C) tensor")
+        need_bwd = any(ctx.needs_input_grad[:8])
+        # Dtypes, devices, widths and weight shapes (tables: rows checked against max_len below).
+        _validate(x[:1].unsqueeze(0), weights, factor1, factor2, H, N, eps, need_bwd)
+        total, C = x.shape
+        if (cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2
+                or cu_seqlens.device != x.device):
+            raise ValueError("cu_seqlens must be a 1-D int32 tensor of nseq + 1 offsets on the device of x")
+        nseq = cu_seqlens.numel() - 1
+        if not 1 <= max_len <= total:
+            raise ValueError(f"max_len={max_len} must be in [1, {total}]")
+        if factor1.shape[0] < max_len:
+            raise ValueError(f"rotary tables have {factor1.shape[0]} rows, fewer than max_len={max_len}")
+        lib = _lib.load()
+        dev = x.device
+        xc = x.contiguous()
+        wc = [w.contiguous() for w in weights]
+        cu = cu_seqlens.contiguous()
+        f1, f2 = _tables32(factor1, factor2, max_len)
+        d = _lib.desc(1, total, C, H, N, max_len, eps)
+        d_ws = _lib.desc(1, total, C, H, N, total, eps)
+        y = torch.empty((total, C), device=dev, dtype=torch.bfloat16)
+        if need_bwd:
+            o_save = torch.empty((total, H * N), device=dev, dtype=torch.bfloat16)
+            lse = torch.empty((H, total), device=dev, dtype=torch.float32)
+        else:
+            o_save = lse = None
+        ws_bytes = lib.mea_workspace_bytes(d_ws, _lib.MEA_PASS_FWD)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        with torch.cuda.device(dev):
+            rc = lib.mea_fwd_varlen(
+                d, cu.data_ptr(), nseq, max_len, xc.data_ptr(), *[w.data_ptr() for w in wc], f1.data_ptr(),
+                f2.data_ptr(), y.data_ptr(), _lib.ptr(o_save), _lib.ptr(lse), ws.data_ptr(), ws_bytes,
+                _lib.stream_of(dev),
+            )
+        _lib.check(rc, "mea_fwd_varlen")
+        if need_bwd:
+            ctx.save_for_backward(xc, *wc, factor1, factor2, cu, o_save, lse)
+        ctx.H, ctx.N, ctx.eps, ctx.max_len = H, N, eps, max_len
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, wq, wk, wv, wg, wo, factor1, factor2, cu, o_save, lse = ctx.saved_tensors
+        H, N, eps, max_len = ctx.H, ctx.N, ctx.eps, ctx.max_len
+        if x.shape[1] > MAX_C_BACKWARD:
+            raise ValueError(f"backward supports C <= {MAX_C_BACKWARD}")
+        lib = _lib.load()
+        total, C = x.shape
+        dev = x.device
+        nseq = cu.numel() - 1
+        dy = grad_output.to(torch.bfloat16).contiguous()
+        f1, f2 = _tables32(factor1, factor2, max_len)
+        d = _lib.desc(1, total, C, H, N, max_len, eps)
+        d_ws = _lib.desc(1, total, C, H, N, total, eps)
+        dx = torch.empty_like(x)
+        dws = [torch.empty_like(w) for w in (wq, wk, wv, wg, wo)]
+        want_f = ctx.needs_input_grad[6] or ctx.needs_input_grad[7]
+        if want_f:
+            df1 = torch.empty((max_len, N), device=dev, dtype=torch.float32)
+            df2 = torch.empty((max_len, N), device=dev, dtype=torch.float32)
+        else:
+            df1 = df2 = None
+        ws_bytes = lib.mea_workspace_bytes(d_ws, _lib.MEA_PASS_BWD)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        with torch.cuda.device(dev):
+            rc = lib.mea_bwd_varlen(
+                d, cu.data_ptr(), nseq, max_len, dy.data_ptr(), x.data_ptr(), wq.data_ptr(), wk.data_ptr(),
+                wv.data_ptr(), wg.data_ptr(), wo.data_ptr(), f1.data_ptr(), f2.data_ptr(), o_save.data_ptr(),
+                lse.data_ptr(), dx.data_ptr(), *[w.data_ptr() for w in dws], _lib.ptr(df1), _lib.ptr(df2),
+                ws.data_ptr(), ws_bytes, _lib.stream_of(dev),
+            )
+        _lib.check(rc, "mea_bwd_varlen")
+        gf1 = gf2 = None
+        if want_f:
+            gf1 = torch.zeros_like(factor1)
+            gf2 = torch.zeros_like(factor2)
+            gf1[:max_len] = df1.to(factor1.dtype)
+            gf2[:max_len] = df2.to(factor2.dtype)
+        return (dx, *dws, gf1, gf2, None, None, None, None, None)
+
+
+def fused_attn_varlen(x, q_proj, k_proj, v_proj, g_proj, o_proj, yarn_module, H, N, cu_seqlens, max_len=None,
+                      eps=1e-6):
+    """``fused_attn`` over packed sequences: x (total, C), cu_seqlens the
+    nseq + 1 int32 offsets (a device tensor, or a list of ints). max_len
+    defaults to the longest sequence (read from the offsets on the host)."""
+    if not isinstance(cu_seqlens, torch.Tensor):
+        lens = list(cu_seqlens)
+        cu_seqlens = torch.tensor(lens, dtype=torch.int32, device=x.device)
+        host = lens
+    else:
+        host = None
+    if max_len is None:
+        host = host if host is not None else cu_seqlens.tolist()
+        max_len = max(b - a for a, b in zip(host[:-1], host[1:]))
+    return FusedAttentionVarlenFunction.apply(
+        x, q_proj.weight, k_proj.weight, v_proj.weight, g_proj.weight, o_proj.weight, yarn_module.factor1,
+        yarn_module.factor2, cu_seqlens, max_len, H, N, eps,
+    )

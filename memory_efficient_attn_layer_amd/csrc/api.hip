@@ -18,7 +18,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 // Byte offsets of every transient inside the workspace.
 struct Layout {
-  size_t q, k, v, sig, o, qkn;               // forward
+  size_t q, k, v, sig, tpos, o, qkn;         // forward (tpos: packed sequences only)
   size_t dO, da;                             // backward; da = [da_q|da_k|da_v|da_g] (M, 4HN)
   size_t rx, rq, rk, delta, woT, wcatT, part;
   size_t total;
@@ -34,6 +34,7 @@ Layout make_layout(const mea_desc& d, int pass) {
   L.k = take(act);
   L.v = take(act);
   L.sig = take(act);
+  L.tpos = take(M * 4);
   if (pass == MEA_PASS_FWD) {
     L.o = take(act);
     L.qkn = take(2 * sizeof(float));
@@ -69,6 +70,30 @@ int validate(const mea_desc* d, int pass) {
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Packed sequences: sequence s holds tokens cu[s] .. cu[s+1]-1 of a B = 1,
+// T = total batch; no sequence is longer than max_len.
+struct Varlen {
+  const int* cu;
+  int nseq, max_len;
+};
+
+// validate() for a pass; with packed sequences the rotary tables need only
+// max_len rows (T is the total token count), B must be 1 and cu a 4-byte
+// aligned device array of nseq + 1 offsets.
+int validate_pass(const mea_desc* d, int pass, const Varlen* var) {
+  if (var == nullptr) return validate(d, pass);
+  if (d == nullptr) return MEA_ERR_NULL;
+  mea_desc dd = *d;
+  dd.T_max = d->T_max > d->T ? d->T_max : d->T;
+  const int rc = validate(&dd, pass);
+  if (rc != MEA_OK) return rc;
+  if (d->B != 1 || var->nseq < 1 || var->max_len < 1 || var->max_len > d->T || d->T_max < var->max_len)
+    return MEA_ERR_SHAPE;
+  if (var->cu == nullptr) return MEA_ERR_NULL;
+  if (((uintptr_t)var->cu & 3u) != 0) return MEA_ERR_ALIGN;
+  return MEA_OK;
+}
 
 int check_ptrs(std::initializer_list<const void*> ps) {
   for (const void* p : ps) {
@@ -155,13 +180,10 @@ namespace {
 // logits come out of the MFMA ready for exp2.
 float q_log2_scale(int64_t N) { return (float)(1.4426950408889634 / sqrt((double)N)); }
 
-int proj_impl(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
-              const float* f1, const float* f2, void* q, void* k, void* v, void* sig, float* rx, float* rq,
-              float* rk, float qscale, float* qk_norm2, void* stream) {
-  int rc = validate(d, MEA_PASS_FWD);
-  if (rc != MEA_OK) return rc;
-  rc = check_ptrs({x, wq, wk, wv, wg, f1, f2, q, k, v, sig});
-  if (rc != MEA_OK) return rc;
+// Launch sequence pieces; the public entry points validate before calling.
+int proj_launch(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+                const float* f1, const float* f2, void* q, void* k, void* v, void* sig, float* rx, float* rq,
+                float* rk, float qscale, float* qk_norm2, const int* tpos, void* stream) {
   mea::ProjParams p;
   p.x = static_cast<const bf16_bits*>(x);
   p.wq = static_cast<const bf16_bits*>(wq);
@@ -179,6 +201,8 @@ int proj_impl(const mea_desc* d, const void* x, const void* wq, const void* wk, 
   p.rk = rk;
   p.qk_norm2 = qk_norm2;
   p.qscale = qscale;
+  p.tpos = tpos;
+  p.t_max = (int)d->T_max;
   p.M = (int)(d->B * d->T);
   p.T = (int)d->T;
   p.C = (int)d->C;
@@ -187,6 +211,16 @@ int proj_impl(const mea_desc* d, const void* x, const void* wq, const void* wk, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   MEA_TRY(timed(K_QKVG_PROJ, s, [&] { return mea::launch_qkvg_proj(p, (int)d->N, s); }));
   return MEA_OK;
+}
+
+int proj_impl(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+              const float* f1, const float* f2, void* q, void* k, void* v, void* sig, float* rx, float* rq,
+              float* rk, float qscale, float* qk_norm2, void* stream) {
+  int rc = validate(d, MEA_PASS_FWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({x, wq, wk, wv, wg, f1, f2, q, k, v, sig});
+  if (rc != MEA_OK) return rc;
+  return proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, qscale, qk_norm2, nullptr, stream);
 }
 
 }  // namespace
@@ -203,12 +237,8 @@ int mea_qkvg_proj(const mea_desc* d, const void* x, const void* wq, const void* 
 
 namespace {
 
-int attn_fwd_impl(const mea_desc* d, const void* q, const void* k, const void* v, void* o, float* lse, float sl2e,
-                  const float* qk_norm2, void* stream) {
-  int rc = validate(d, MEA_PASS_FWD);
-  if (rc != MEA_OK) return rc;
-  rc = check_ptrs({q, k, v, o});
-  if (rc != MEA_OK) return rc;
+int attn_fwd_launch(const mea_desc* d, const void* q, const void* k, const void* v, void* o, float* lse, float sl2e,
+                    const float* qk_norm2, const Varlen* var, void* stream) {
   mea::AttnFwdParams p;
   p.q = static_cast<const bf16_bits*>(q);
   p.k = static_cast<const bf16_bits*>(k);
@@ -220,8 +250,34 @@ int attn_fwd_impl(const mea_desc* d, const void* q, const void* k, const void* v
   p.T = (int)d->T;
   p.sl2e = sl2e;
   p.qk_norm2 = qk_norm2;
+  p.cu = var != nullptr ? var->cu : nullptr;
+  p.nseq = var != nullptr ? var->nseq : 0;
+  p.max_len = var != nullptr ? var->max_len : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   MEA_TRY(timed(K_ATTN_FWD, s, [&] { return mea::launch_attn_fwd(p, (int)d->N, s); }));
+  return MEA_OK;
+}
+
+int attn_fwd_impl(const mea_desc* d, const void* q, const void* k, const void* v, void* o, float* lse, float sl2e,
+                  const float* qk_norm2, void* stream) {
+  int rc = validate(d, MEA_PASS_FWD);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({q, k, v, o});
+  if (rc != MEA_OK) return rc;
+  return attn_fwd_launch(d, q, k, v, o, lse, sl2e, qk_norm2, nullptr, stream);
+}
+
+int gate_oproj_launch(const mea_desc* d, const void* o, const void* sig, const void* wo, void* y, void* stream) {
+  mea::OprojParams p;
+  p.o = static_cast<const bf16_bits*>(o);
+  p.sig = static_cast<const bf16_bits*>(sig);
+  p.wo = static_cast<const bf16_bits*>(wo);
+  p.y = static_cast<bf16_bits*>(y);
+  p.M = (int)(d->B * d->T);
+  p.C = (int)d->C;
+  p.HN = (int)(d->H * d->N);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MEA_TRY(timed(K_GATE_OPROJ, s, [&] { return mea::launch_gate_oproj(p, s); }));
   return MEA_OK;
 }
 
@@ -239,23 +295,17 @@ int mea_gate_oproj(const mea_desc* d, const void* o, const void* sig, const void
   if (rc != MEA_OK) return rc;
   rc = check_ptrs({o, sig, wo, y});
   if (rc != MEA_OK) return rc;
-  mea::OprojParams p;
-  p.o = static_cast<const bf16_bits*>(o);
-  p.sig = static_cast<const bf16_bits*>(sig);
-  p.wo = static_cast<const bf16_bits*>(wo);
-  p.y = static_cast<bf16_bits*>(y);
-  p.M = (int)(d->B * d->T);
-  p.C = (int)d->C;
-  p.HN = (int)(d->H * d->N);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  MEA_TRY(timed(K_GATE_OPROJ, s, [&] { return mea::launch_gate_oproj(p, s); }));
-  return MEA_OK;
+  return gate_oproj_launch(d, o, sig, wo, y, stream);
 }
 
-int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
-            const void* wo, const float* f1, const float* f2, void* y, void* o_save, float* lse_save, void* ws,
-            size_t ws_bytes, void* stream) {
-  int rc = validate(d, MEA_PASS_FWD);
+}  // extern "C"
+
+namespace {
+
+int fwd_impl(const mea_desc* d, const Varlen* var, const void* x, const void* wq, const void* wk, const void* wv,
+             const void* wg, const void* wo, const float* f1, const float* f2, void* y, void* o_save,
+             float* lse_save, void* ws, size_t ws_bytes, void* stream) {
+  int rc = validate_pass(d, MEA_PASS_FWD, var);
   if (rc != MEA_OK) return rc;
   rc = check_ptrs({x, wq, wk, wv, wg, wo, f1, f2, y, ws});
   if (rc != MEA_OK) return rc;
@@ -274,18 +324,23 @@ int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk, co
   MEA_TRY(timed(K_ZERO, static_cast<hipStream_t>(stream),
                 [&] { return mea::launch_zero_f32(qkn, 2, static_cast<hipStream_t>(stream)); }));
   const float qs = q_log2_scale(d->N);
-  rc = proj_impl(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, nullptr, nullptr, nullptr, qs, qkn, stream);
+  int* tpos = nullptr;
+  if (var != nullptr) {
+    tpos = at<int>(ws, L.tpos);
+    MEA_TRY(mea::launch_token_positions(var->cu, var->nseq, (int)d->T, tpos, static_cast<hipStream_t>(stream)));
+  }
+  rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, nullptr, nullptr, nullptr, qs, qkn, tpos, stream);
   if (rc != MEA_OK) return rc;
-  rc = attn_fwd_impl(d, q, k, v, o, lse_save, 1.0f, qkn, stream);
+  rc = attn_fwd_launch(d, q, k, v, o, lse_save, 1.0f, qkn, var, stream);
   if (rc != MEA_OK) return rc;
-  return mea_gate_oproj(d, o, sig, wo, y, stream);
+  return gate_oproj_launch(d, o, sig, wo, y, stream);
 }
 
-int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, const void* wk, const void* wv,
-            const void* wg, const void* wo, const float* f1, const float* f2, const void* o_save,
-            const float* lse_save, void* dx, void* dwq, void* dwk, void* dwv, void* dwg, void* dwo, float* df1,
-            float* df2, void* ws, size_t ws_bytes, void* stream) {
-  int rc = validate(d, MEA_PASS_BWD);
+int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x, const void* wq, const void* wk,
+             const void* wv, const void* wg, const void* wo, const float* f1, const float* f2, const void* o_save,
+             const float* lse_save, void* dx, void* dwq, void* dwk, void* dwv, void* dwg, void* dwo, float* df1,
+             float* df2, void* ws, size_t ws_bytes, void* stream) {
+  int rc = validate_pass(d, MEA_PASS_BWD, var);
   if (rc != MEA_OK) return rc;
   rc = check_ptrs({dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, dx, dwq, dwk, dwv, dwg, dwo, ws});
   if (rc != MEA_OK) return rc;
@@ -323,13 +378,20 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
       return mea::launch_transpose(static_cast<const bf16_bits*>(wp[j]), HN, C, C, wcatT, 4 * HN, j * HN, s);
     }));
   if (df1 != nullptr) {
-    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df1, (size_t)T * N, s); }));
-    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df2, (size_t)T * N, s); }));
+    // Table rows the block touches: positions 0 .. T-1 (packed: max_len - 1).
+    const size_t rows = (size_t)(var != nullptr ? var->max_len : T);
+    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df1, rows * N, s); }));
+    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df2, rows * N, s); }));
   }
 
   // Recompute q, k, v, sigmoid(g) and the three RMS statistics.
   const float qs = q_log2_scale(N);
-  rc = proj_impl(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, qs, nullptr, stream);
+  int* tpos = nullptr;
+  if (var != nullptr) {
+    tpos = at<int>(ws, L.tpos);
+    MEA_TRY(mea::launch_token_positions(var->cu, var->nseq, T, tpos, s));
+  }
+  rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, qs, nullptr, tpos, stream);
   if (rc != MEA_OK) return rc;
 
   mea::DzParams dz;
@@ -373,6 +435,9 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   ab.scale = (float)(1.0 / sqrt((double)N));
   ab.sl2e = 1.0f;  // q was stored in log2 units by the recompute above
   ab.qscale = qs;
+  ab.cu = var != nullptr ? var->cu : nullptr;
+  ab.nseq = var != nullptr ? var->nseq : 0;
+  ab.max_len = var != nullptr ? var->max_len : 0;
   MEA_TRY(timed(K_ATTN_BWD_DQ, s, [&] { return mea::launch_attn_bwd_dq(ab, N, s); }));
   MEA_TRY(timed(K_ATTN_BWD_DKDV, s, [&] { return mea::launch_attn_bwd_dkdv(ab, N, s); }));
 
@@ -410,6 +475,42 @@ int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, co
   dxp.HN = HN;
   MEA_TRY(timed(K_DX, s, [&] { return mea::launch_dx(dxp, s); }));
   return MEA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+            const void* wo, const float* f1, const float* f2, void* y, void* o_save, float* lse_save, void* ws,
+            size_t ws_bytes, void* stream) {
+  return fwd_impl(d, nullptr, x, wq, wk, wv, wg, wo, f1, f2, y, o_save, lse_save, ws, ws_bytes, stream);
+}
+
+int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq, const void* wk, const void* wv,
+            const void* wg, const void* wo, const float* f1, const float* f2, const void* o_save,
+            const float* lse_save, void* dx, void* dwq, void* dwk, void* dwv, void* dwg, void* dwo, float* df1,
+            float* df2, void* ws, size_t ws_bytes, void* stream) {
+  return bwd_impl(d, nullptr, dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, dx, dwq, dwk, dwv, dwg, dwo, df1,
+                  df2, ws, ws_bytes, stream);
+}
+
+int mea_fwd_varlen(const mea_desc* d, const int32_t* cu_seqlens, int32_t nseq, int32_t max_len, const void* x,
+                   const void* wq, const void* wk, const void* wv, const void* wg, const void* wo, const float* f1,
+                   const float* f2, void* y, void* o_save, float* lse_save, void* ws, size_t ws_bytes,
+                   void* stream) {
+  const Varlen var{cu_seqlens, nseq, max_len};
+  return fwd_impl(d, &var, x, wq, wk, wv, wg, wo, f1, f2, y, o_save, lse_save, ws, ws_bytes, stream);
+}
+
+int mea_bwd_varlen(const mea_desc* d, const int32_t* cu_seqlens, int32_t nseq, int32_t max_len, const void* dy,
+                   const void* x, const void* wq, const void* wk, const void* wv, const void* wg, const void* wo,
+                   const float* f1, const float* f2, const void* o_save, const float* lse_save, void* dx, void* dwq,
+                   void* dwk, void* dwv, void* dwg, void* dwo, float* df1, float* df2, void* ws, size_t ws_bytes,
+                   void* stream) {
+  const Varlen var{cu_seqlens, nseq, max_len};
+  return bwd_impl(d, &var, dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, dx, dwq, dwk, dwv, dwg, dwo, df1,
+                  df2, ws, ws_bytes, stream);
 }
 
 int mea_prefill(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,

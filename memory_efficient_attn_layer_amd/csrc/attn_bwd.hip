@@ -36,14 +36,13 @@ namespace mea {
 //   rotary == 0 : plain copy (v).
 // Output row t goes to out[(b*T + t)*ld_da + h*N ...], scaled by rx[b*T + t].
 template <int N>
-__device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, const AttnBwdParams& p,
-                                             int b, int h, bool rotary, const bf16_bits* xrot, float xscale,
-                                             const float* rstat, bf16_bits* out) {
+__device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, const AttnBwdParams& p, int T,
+                                             size_t tok_row0, size_t head_row0, int h, bool rotary,
+                                             const bf16_bits* xrot, float xscale, const float* rstat,
+                                             bf16_bits* out) {
   constexpr int CPR = N / 8, RPP = 64 / CPR;
   const int lane = threadIdx.x & 63;
-  const int T = p.T, H = p.H;
   const size_t ld = (size_t)p.ld_da;
-  const size_t bh = (size_t)b * H + h;
 #pragma unroll 1
   for (int pass = 0; pass < 32 / RPP; ++pass) {
     const int row = pass * RPP + lane / CPR, dc = lane % CPR;
@@ -57,11 +56,11 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 #pragma unroll
       for (int i = 0; i < 4; ++i) { dv[i] = a[i]; dv[4 + i] = c[i]; }
     }
-    const float rxv = p.rx[(size_t)b * T + tc];
+    const float rxv = p.rx[tok_row0 + tc];
     float res[8];
     if (rotary) {
       float xv[8], a1[8], a2[8];
-      unpack8(ld16(xrot + (bh * T + tc) * N + dc * 8), xv);
+      unpack8(ld16(xrot + (head_row0 + tc) * N + dc * 8), xv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[i] *= xscale;
       const float* f1r = p.f1 + (size_t)tc * N + dc * 8;
@@ -89,7 +88,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
       dot += xor2(dot);
       dot += shfl_xor(dot, 4);
       if (CPR == 16) dot += shfl_xor(dot, 8);
-      const float rr = rstat[bh * T + tc];
+      const float rr = rstat[head_row0 + tc];
       const float sc = rxv * rr, cf = dot / (float)N;
 #pragma unroll
       for (int i = 0; i < 8; ++i) res[i] = sc * (dh[i] - xh[i] * cf);
@@ -106,7 +105,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 #pragma unroll
       for (int i = 0; i < 8; ++i) res[i] = rxv * dv[i];
     }
-    if (valid) st16(out + ((size_t)b * T + t) * ld + (size_t)h * N + dc * 8, pack8(res));
+    if (valid) st16(out + (tok_row0 + t) * ld + (size_t)h * N + dc * 8, pack8(res));
   }
 }
 
@@ -129,7 +128,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // double-buffered, one barrier per tile); tiles below the workgroup's first
 // query run in a branch-free loop, the diagonal region after it.
 // ---------------------------------------------------------------------------
-template <int N>
+template <int N, bool VARLEN>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   constexpr int QW = N == 64 ? 64 : 32;  // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
@@ -146,19 +145,41 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char smem_raw[SMEM];
   bf16_bits* smem = reinterpret_cast<bf16_bits*>(smem_raw);
 
-  const int T = p.T, BH = p.B * p.H;
-  const int nqb = (T + BQ - 1) / BQ;
   // Each XCD walks whole heads (heaviest query block first), so the K/V
-  // tiles of a head are fetched once into that XCD's L2.
-  const int lid = xcd_remap(blockIdx.x, BH * nqb);
-  const int bh = lid / nqb, qi = nqb - 1 - lid % nqb;
-  const int b = bh / p.H, hd = bh % p.H;
+  // tiles of a head are fetched once into that XCD's L2. VARLEN: packed
+  // sequences (p.cu), rows relative to the sequence's first token.
+  int T, bh, qi, b, hd;
+  size_t head_row0, tok_row0;
+  if constexpr (!VARLEN) {
+    T = p.T;
+    const int nqb = (T + BQ - 1) / BQ;
+    const int lid = xcd_remap(blockIdx.x, p.B * p.H * nqb);
+    bh = lid / nqb;
+    qi = nqb - 1 - lid % nqb;
+    b = bh / p.H;
+    hd = bh % p.H;
+    head_row0 = (size_t)bh * T;
+    tok_row0 = (size_t)b * T;
+  } else {
+    const int nqb = (p.max_len + BQ - 1) / BQ;
+    const int lid = xcd_remap(blockIdx.x, p.nseq * p.H * nqb);
+    bh = lid / nqb;
+    qi = nqb - 1 - lid % nqb;
+    b = bh / p.H;
+    hd = bh % p.H;
+    // Offsets clamped to [0, total]: a malformed list cannot index outside.
+    const int start = min(max(p.cu[b], 0), p.T);
+    T = min(max(p.cu[b + 1], start), p.T) - start;
+    head_row0 = (size_t)hd * p.T + start;
+    tok_row0 = (size_t)start;
+    if (qi * BQ >= T) return;  // past this sequence's end: uniform, before any barrier
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, h = lane >> 5;
   const int q0w = qi * BQ + wave * QW;
   const int kv_end = min(T, qi * BQ + BQ);
-  const size_t head_off = (size_t)bh * T * N;
+  const size_t head_off = head_row0 * N;
   const bf16_bits* kg = p.k + head_off;
   const bf16_bits* vg = p.v + head_off;
 
@@ -179,7 +200,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
       qf[qb][ks] = as_frag(ld16(p.q + off));
       df[qb][ks] = as_frag(ld16(p.dO + off));
     }
-    const u32x4 sw = stat_pack(-p.lse[(size_t)bh * T + t] * kLog2e, -p.delta[(size_t)bh * T + t]);
+    const u32x4 sw = stat_pack(-p.lse[head_row0 + t] * kLog2e, -p.delta[head_row0 + t]);
     stat[qb * 64 + lane] = h == 0 ? sw : u32x4{0u, 0u, 0u, 0u};
   }
   const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
@@ -320,7 +341,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   __syncthreads();
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb)
-    head_row_bwd<N>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, b, hd, true, p.q, 1.0f / p.qscale, p.rq, p.daq);
+    head_row_bwd<N>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, T, tok_row0, head_row0, hd, true, p.q,
+                    1.0f / p.qscale, p.rq, p.daq);
 }
 
 // ---------------------------------------------------------------------------
@@ -343,7 +365,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 // (global_load_lds, double-buffered, one barrier per tile), starting at the
 // block's first key (causal).
 // ---------------------------------------------------------------------------
-template <int N>
+template <int N, bool VARLEN>
 __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
   constexpr int KW = 32;                 // keys per wave
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
@@ -363,17 +385,39 @@ __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(Att
   // one zero block read by the lanes that hold k-elements 8..15.
   u32x4* stats = reinterpret_cast<u32x4*>(smem + 2 * 2 * TILE * 2);
 
-  const int T = p.T, BH = p.B * p.H;
-  const int nkb = (T + BKV - 1) / BKV;
   // Each XCD walks whole heads, the key block that sees the most queries
-  // first, so the Q/dO tiles of a head are shared in one L2.
-  const int lid = xcd_remap(blockIdx.x, BH * nkb);
-  const int bh = lid / nkb, ki = lid % nkb;
-  const int b = bh / p.H, hd = bh % p.H;
+  // first, so the Q/dO tiles of a head are shared in one L2. VARLEN: packed
+  // sequences (p.cu), rows relative to the sequence's first token.
+  int T, bh, ki, b, hd;
+  size_t head_row0, tok_row0;
+  if constexpr (!VARLEN) {
+    T = p.T;
+    const int nkb = (T + BKV - 1) / BKV;
+    const int lid = xcd_remap(blockIdx.x, p.B * p.H * nkb);
+    bh = lid / nkb;
+    ki = lid % nkb;
+    b = bh / p.H;
+    hd = bh % p.H;
+    head_row0 = (size_t)bh * T;
+    tok_row0 = (size_t)b * T;
+  } else {
+    const int nkb = (p.max_len + BKV - 1) / BKV;
+    const int lid = xcd_remap(blockIdx.x, p.nseq * p.H * nkb);
+    bh = lid / nkb;
+    ki = lid % nkb;
+    b = bh / p.H;
+    hd = bh % p.H;
+    // Offsets clamped to [0, total]: a malformed list cannot index outside.
+    const int start = min(max(p.cu[b], 0), p.T);
+    T = min(max(p.cu[b + 1], start), p.T) - start;
+    head_row0 = (size_t)hd * p.T + start;
+    tok_row0 = (size_t)start;
+    if (ki * BKV >= T) return;  // past this sequence's end: uniform, before any barrier
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, h = lane >> 5;
   const int k0 = ki * BKV, kw0 = k0 + wave * KW;
-  const size_t head_off = (size_t)bh * T * N;
+  const size_t head_off = head_row0 * N;
   const bf16_bits* qg = p.q + head_off;
   const bf16_bits* dg = p.dO + head_off;
 
@@ -402,7 +446,7 @@ __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(Att
       g2lds16(dg + off, qt + TILE + (u * 4 + wave) * 512);
     }
     if (tid < BQ) {
-      const size_t t = (size_t)bh * T + min(q0 + tid, T - 1);
+      const size_t t = head_row0 + min(q0 + tid, T - 1);
       st_l = p.lse[t];
       st_d = p.delta[t];
     }
@@ -562,7 +606,7 @@ __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(Att
         *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v;
       }
     __syncthreads();
-    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, b, hd, false, nullptr, 1.0f, nullptr, p.dav);
+    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, hd, false, nullptr, 1.0f, nullptr, p.dav);
     __syncthreads();
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -572,7 +616,7 @@ __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(Att
         *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v * (p.scale / p.qscale);
       }
     __syncthreads();
-    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, b, hd, true, p.k, 1.0f, p.rk, p.dak);
+    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, hd, true, p.k, 1.0f, p.rk, p.dak);
     __syncthreads();
   }
 }
@@ -580,22 +624,32 @@ __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(Att
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
   if (p.sl2e != 1.0f) return hipErrorInvalidValue;  // stored q must be in log2 units
   const int BQ = N == 64 ? 256 : 128;
-  const int G = p.B * p.H * ((p.T + BQ - 1) / BQ);
-  if (N == 64)
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, dim3(G), dim3(256), 0, s, p);
+  const bool var = p.cu != nullptr;
+  const int G = var ? p.nseq * p.H * ((p.max_len + BQ - 1) / BQ) : p.B * p.H * ((p.T + BQ - 1) / BQ);
+  if (N == 64 && !var)
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
+  else if (N == 64)
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
+  else if (!var)
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<128>, dim3(G), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s) {
   if (p.sl2e != 1.0f) return hipErrorInvalidValue;  // stored q must be in log2 units
   const int BKV = 128;
-  const int G = p.B * p.H * ((p.T + BKV - 1) / BKV);
-  if (N == 64)
-    hipLaunchKernelGGL(attn_bwd_dkdv_kernel<64>, dim3(G), dim3(256), 0, s, p);
+  const bool var = p.cu != nullptr;
+  const int G = var ? p.nseq * p.H * ((p.max_len + BKV - 1) / BKV) : p.B * p.H * ((p.T + BKV - 1) / BKV);
+  if (N == 64 && !var)
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
+  else if (N == 64)
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
+  else if (!var)
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(attn_bwd_dkdv_kernel<128>, dim3(G), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -40,7 +40,10 @@
 
 namespace mea {
 
-template <int N>
+// VARLEN: packed sequences (p.cu); a workgroup's (b, h, query block) becomes
+// (sequence, h, query block) and every row index is taken relative to the
+// sequence's first token.
+template <int N, bool VARLEN>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   constexpr int QW = N == 64 ? 64 : 32;  // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
@@ -56,19 +59,40 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   constexpr int SMEM = 4 * TILE > 4 * QW * OP ? 4 * TILE : 4 * QW * OP;
   __shared__ __attribute__((aligned(16))) bf16_bits smem[SMEM];  // [stage][K | V], then output staging
 
-  const int T = p.T, BH = p.B * p.H;
-  const int nqb = (T + BQ - 1) / BQ;
   // Each XCD walks whole heads (heaviest query block of a head first), so
   // the K/V tiles of a head are fetched once into that XCD's L2.
-  const int lid = xcd_remap(blockIdx.x, BH * nqb);
-  const int bh = lid / nqb, qi = nqb - 1 - lid % nqb;
-  const int b = bh / p.H, hd = bh % p.H;
+  int T, bh, qi, b, hd;
+  size_t head_row0, tok_row0;  // first row of the (b, h) sequence in (B*H, T) / (B*T) order
+  if constexpr (!VARLEN) {
+    T = p.T;
+    const int nqb = (T + BQ - 1) / BQ;
+    const int lid = xcd_remap(blockIdx.x, p.B * p.H * nqb);
+    bh = lid / nqb;
+    qi = nqb - 1 - lid % nqb;
+    b = bh / p.H;
+    hd = bh % p.H;
+    head_row0 = (size_t)bh * T;
+    tok_row0 = (size_t)b * T;
+  } else {
+    const int nqb = (p.max_len + BQ - 1) / BQ;
+    const int lid = xcd_remap(blockIdx.x, p.nseq * p.H * nqb);
+    bh = lid / nqb;  // sequence-major (s, h)
+    qi = nqb - 1 - lid % nqb;
+    b = bh / p.H;
+    hd = bh % p.H;
+    // Offsets clamped to [0, total]: a malformed list cannot index outside.
+    const int start = min(max(p.cu[b], 0), p.T);
+    T = min(max(p.cu[b + 1], start), p.T) - start;
+    head_row0 = (size_t)hd * p.T + start;
+    tok_row0 = (size_t)start;
+    if (qi * BQ >= T) return;  // past this sequence's end: uniform, before any barrier
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, h = lane >> 5;
   const int q0w = qi * BQ + wave * QW;
   const int kv_end = min(T, qi * BQ + BQ);
-  const size_t head_off = (size_t)bh * T * N;
+  const size_t head_off = head_row0 * N;
   const bf16_bits* kg = p.k + head_off;
   const bf16_bits* vg = p.v + head_off;
 
@@ -374,7 +398,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     const float l = l_i[qb] + __shfl_xor(l_i[qb], 32, 64);
     const float inv = 1.0f / l;
     const int qq = q0w + 32 * qb + c;
-    if (p.lse != nullptr && h == 0 && qq < T) p.lse[(size_t)bh * T + qq] = (m_i[qb] + __log2f(l)) * kLn2;
+    if (p.lse != nullptr && h == 0 && qq < T) p.lse[head_row0 + qq] = (m_i[qb] + __log2f(l)) * kLn2;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -392,18 +416,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     const int t = q0w + row;
     if (t < T) {
       const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * OP + dc * 8);
-      st16(p.o + ((size_t)b * T + t) * HN + (size_t)hd * N + dc * 8, val);
+      st16(p.o + (tok_row0 + t) * HN + (size_t)hd * N + dc * 8, val);
     }
   }
 }
 
 hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s) {
   const int BQ = N == 64 ? 256 : 128;
-  const int G = p.B * p.H * ((p.T + BQ - 1) / BQ);
-  if (N == 64)
-    hipLaunchKernelGGL(attn_fwd_kernel<64>, dim3(G), dim3(256), 0, s, p);
+  const bool var = p.cu != nullptr;
+  const int G = var ? p.nseq * p.H * ((p.max_len + BQ - 1) / BQ) : p.B * p.H * ((p.T + BQ - 1) / BQ);
+  if (N == 64 && !var)
+    hipLaunchKernelGGL((attn_fwd_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
+  else if (N == 64)
+    hipLaunchKernelGGL((attn_fwd_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
+  else if (!var)
+    hipLaunchKernelGGL((attn_fwd_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(attn_fwd_kernel<128>, dim3(G), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attn_fwd_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

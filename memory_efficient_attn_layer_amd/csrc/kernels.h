@@ -21,11 +21,18 @@ struct ProjParams {
   // Largest squared norms of the stored q and k rows (2 floats, zeroed
   // beforehand, raised with atomic max) or null.
   float* qk_norm2;
+  // Rotary row of every token (M), or null (row = t of the (B, T) layout):
+  // packed sequences give each token its position inside its sequence.
+  const int* tpos;
+  int t_max;                                // rows of f1 / f2 (tpos is clamped to it)
   int M, T, C, H;
   float eps;
   float qscale;                             // the stored q rows are q * qscale
 };
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s);
+
+// tpos[m] = m - cu[s] for cu[s] <= m < cu[s+1] (packed sequences).
+hipError_t launch_token_positions(const int* cu, int nseq, int M, int* tpos, hipStream_t s);
 
 // Causal flash attention forward.
 struct AttnFwdParams {
@@ -37,6 +44,11 @@ struct AttnFwdParams {
   const float* qk_norm2;
   int B, H, T;
   float sl2e;                               // multiplies q.k into log2 units
+  // Packed sequences (or null): sequence s holds tokens cu[s] .. cu[s+1]-1 of
+  // a (1, H, T, N) / (T, H*N) layout with T the total; nseq sequences of at
+  // most max_len tokens. Attention stays inside each sequence.
+  const int* cu;
+  int nseq, max_len;
 };
 constexpr float kFixedBound = 60.0f;
 hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s);
@@ -56,6 +68,8 @@ struct AttnBwdParams {
   float scale;                              // softmax scale 1/sqrt(N)
   float sl2e;                               // must be 1: stored q . k is in log2 units
   float qscale;                             // stored q = q * qscale
+  const int* cu;                            // packed sequences, as in AttnFwdParams (or null)
+  int nseq, max_len;
 };
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s);
 hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s);

@@ -55,7 +55,9 @@ __device__ __forceinline__ ProjTile proj_tile(int L, int H) {
 // Persistent: workgroups walk tiles; workgroup w runs on XCD w % 8 and takes
 // tiles from a contiguous range owned by that XCD, so the workgroups of one
 // XCD work on neighbouring tiles at the same time.
-template <int N>
+// POS: every token reads its rotary row from p.tpos (packed sequences); a
+// separate instantiation, so the (B, T) kernel keeps its code.
+template <int N, bool POS>
 __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   constexpr int BT = kProjBT, BF = kProjBF, BK = kProjBK, NS = kProjStages;
   constexpr int STAGE = (BF + BT) * BK;
@@ -194,6 +196,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     const bool has_rot = N == 64 || tl.f0 == 0;  // the wave holds q or k
     auto tab_row = [&](int tb) {
       const int m = m0 + wt * (TB * 16) + tb * 16 + c16;
+      if (POS) return min(max(p.tpos[min(m, M - 1)], 0), p.t_max - 1);
       return tile_whole ? t0 + (m - m0) : (m < M ? m - (m / T) * T : 0);
     };
     // N = 64: one slot of table rows, filled for block 0 at the start of the
@@ -412,10 +415,40 @@ int persistent_grid(int tiles, int per_cu) {
 
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s) {
   const int G = persistent_grid(((p.M + kProjBT - 1) / kProjBT) * p.H * (4 * N / kProjBF), 2);
-  if (N == 64)
-    hipLaunchKernelGGL(qkvg_proj_kernel<64>, dim3(G), dim3(256), 0, s, p);
+  const bool pos = p.tpos != nullptr;
+  if (N == 64 && !pos)
+    hipLaunchKernelGGL((qkvg_proj_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
+  else if (N == 64)
+    hipLaunchKernelGGL((qkvg_proj_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
+  else if (!pos)
+    hipLaunchKernelGGL((qkvg_proj_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(qkvg_proj_kernel<128>, dim3(G), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((qkvg_proj_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+namespace {
+
+// One thread per token: the sequence holding token m by binary search over
+// the nseq + 1 offsets cu (cu[0] = 0, increasing).
+__global__ __launch_bounds__(256) void token_positions_kernel(const int* cu, int nseq, int M, int* tpos) {
+  const int m = blockIdx.x * 256 + threadIdx.x;
+  if (m >= M) return;
+  int lo = 0, hi = nseq;  // cu[lo] <= m < cu[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cu[mid] <= m)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  tpos[m] = m - cu[lo];
+}
+
+}  // namespace
+
+hipError_t launch_token_positions(const int* cu, int nseq, int M, int* tpos, hipStream_t s) {
+  hipLaunchKernelGGL(token_positions_kernel, dim3((M + 255) / 256), dim3(256), 0, s, cu, nseq, M, tpos);
   return hipGetLastError();
 }
 

@@ -144,6 +144,31 @@ def test_decode_and_prefill_validation(lib):
     assert lib.mea_prefill(ctypes.byref(pd), *p_no_cache, 128, fake, 1 << 40, None) == _header_enum("MEA_ERR_NULL")
 
 
+def test_varlen_validation(lib):
+    fake = 1 << 20  # aligned, never dereferenced: validation fails first
+    # fwd pointers after (cu, nseq, max_len): x wq wk wv wg wo f1 f2 y o lse ws
+    fargs = [fake] * 12
+    # T (total tokens) may exceed T_max: the tables need max_len rows only.
+    d = _d(B=1, T=1000, T_max=300)
+    ok_shape = lib.mea_fwd_varlen(ctypes.byref(d), fake, 4, 300, *fargs, 10, None)
+    assert ok_shape == _header_enum("MEA_ERR_WORKSPACE")
+    for dd, nseq, max_len, code in [
+        (_d(B=2, T=1000, T_max=300), 4, 300, "MEA_ERR_SHAPE"),  # packed batches have B = 1
+        (d, 0, 300, "MEA_ERR_SHAPE"),
+        (d, 4, 301, "MEA_ERR_SHAPE"),                            # longer than the tables
+        (_d(B=1, T=200, T_max=300), 4, 250, "MEA_ERR_SHAPE"),    # longer than the total
+        (d, 4, 0, "MEA_ERR_SHAPE"),
+    ]:
+        assert lib.mea_fwd_varlen(ctypes.byref(dd), fake, nseq, max_len, *fargs, 10, None) == _header_enum(code)
+    assert lib.mea_fwd_varlen(ctypes.byref(d), None, 4, 300, *fargs, 10, None) == _header_enum("MEA_ERR_NULL")
+    assert lib.mea_fwd_varlen(ctypes.byref(d), fake + 2, 4, 300, *fargs, 10, None) == _header_enum("MEA_ERR_ALIGN")
+    # bwd: dy x wq wk wv wg wo f1 f2 o lse dx dwq dwk dwv dwg dwo df1 df2 ws
+    bargs = [fake] * 20
+    assert lib.mea_bwd_varlen(ctypes.byref(d), fake, 4, 300, *bargs, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
+    assert lib.mea_bwd_varlen(ctypes.byref(_d(B=1, T=1000, T_max=300, C=2048)), fake, 4, 300, *bargs, 1 << 40,
+                              None) == _header_enum("MEA_ERR_MODEL_DIM")
+
+
 def _cpu_args(B=1, T=8, C=256, H=4, N=64, dtype=torch.bfloat16):
     HN = H * N
     x = torch.randn(B, T, C, dtype=dtype)
