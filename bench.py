@@ -15,6 +15,7 @@ batch slice on the host cores). Progress goes to stderr.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--compare-eager] [--no-cpu-baseline]
     python bench.py --workload 2|3       # the same line for another fwd+bwd workload
     python bench.py --workload 4         # forward-only (prefill) workload: fwd tokens/s, no CPU leg
+    python bench.py --workload W --varlen  # B packed sequences of seeded lengths in [T/4, T], fwd+bwd
     python bench.py --workload W --decode [--context L]
                                          # KV-cache decode steps at context L (default T - 1)
     python bench.py --copy-calibration   # a plain 256 MiB device copy, for HBM counter scaling
@@ -159,6 +160,8 @@ def main():
     ap.add_argument("--compare-eager", action="store_true", help="also time the eager SDPA path on the GPU")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--varlen", action="store_true",
+                    help="pack B sequences of seeded random lengths in [T/4, T] (fwd+bwd, packed-sequence path)")
     ap.add_argument("--decode", action="store_true",
                     help="time KV-cache decode steps (one token per sequence) instead of fwd+bwd")
     ap.add_argument("--context", type=int, default=None, help="decode: cached tokens per sequence (default T - 1)")
@@ -189,6 +192,9 @@ def main():
     w = WORKLOADS[args.workload]
     if args.decode:
         decode_bench(args, w)
+        return
+    if args.varlen:
+        varlen_bench(args, w)
         return
     if not w.backward:
         forward_bench(args, w)
@@ -375,6 +381,88 @@ def forward_bench(args, w):
                    "tokens_per_step": tokens, "parallelism": "single-gpu"},
         "peak_hbm": {"fused_bytes": int(peak)},
         "block_tflops": round(w.flops_fwd() / sec / 1e12, 2),
+        "roofline": roofline_of(prof, work),
+        "kernels": kernels,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def varlen_bench(args, w):
+    """Packed sequences: the workload's B sequences get seeded random lengths
+    in [T/4, T] and run back to back through the packed-sequence entry points
+    (one forward and one backward per step). Algorithmic attention flops are
+    summed per sequence."""
+    import torch
+
+    from memory_efficient_attn_layer_amd import _lib
+    from memory_efficient_attn_layer_amd.attention import FusedAttentionVarlenFunction
+    from memory_efficient_attn_layer_amd.synthetic import make_inputs
+
+    g = torch.Generator().manual_seed(4242)
+    lens = torch.randint(w.T // 4, w.T + 1, (w.B,), generator=g).tolist()
+    total = sum(lens)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"workload {w.name}: {w.B} packed sequences, {total} tokens (lengths {min(lens)}..{max(lens)})")
+    inp = make_inputs(w, device=dev)
+    x = inp["x"].reshape(-1, w.C)[:total].contiguous().requires_grad_(True)
+    dy = inp["dy"].reshape(-1, w.C)[:total].contiguous()
+    ws = [inp[n].requires_grad_(True) for n in ("wq", "wk", "wv", "wg", "wo")]
+    f1, f2 = inp["f1"], inp["f2"]
+    del inp
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    H, N, L = w.H, w.N, max(lens)
+    sync = torch.cuda.synchronize
+
+    def step():
+        y = FusedAttentionVarlenFunction.apply(x, *ws, f1, f2, cu, L, H, N, 1e-6)
+        return torch.autograd.grad(y, [x, *ws], dy)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    sync()
+    peak = peak_of(step, sync)
+    _lib.profile_enable(True)
+    sec = measure(step, args.steps, 0, sync)
+    _lib.profile_enable(False)
+    prof = _lib.profile_read()
+    pair = sum(2.0 * H * N * n * (n + 1) / 2 for n in lens)
+    M, HN, C = total, H * N, w.C
+    work = kernel_work(w)
+    for k in ("qkvg_proj", "gate_oproj", "dz_gate_bwd", "dw_partial", "dx"):
+        work[k] = dict(work[k], flops=work[k]["flops"] * M / (w.B * w.T))
+    work["attn_fwd"] = dict(work["attn_fwd"], flops=2 * pair)
+    work["attn_bwd_dq"] = dict(work["attn_bwd_dq"], flops=pair)
+    work["attn_bwd_dkdv"] = dict(work["attn_bwd_dkdv"], flops=3 * pair)
+    kernels = {}
+    for name, (cnt, tot) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        avg = tot / cnt
+        ent = {"launches_per_step": cnt / args.steps, "avg_ms": round(avg, 4), "share": round(tot / (sec * 1e3 * args.steps), 4)}
+        if name in work:
+            ent["tflops"] = round(work[name]["flops"] / (avg * 1e-3) / 1e12, 2)
+        kernels[name] = ent
+        log(f"  {name:15s} {avg:8.4f} ms x{cnt / args.steps:.0f}  {ent.get('tflops', '-')} TFLOP/s")
+    flops = 3 * (2.0 * M * C * 4 * HN + 2 * pair + 2.0 * M * HN * C)
+    log(f"{sec * 1e3:.3f} ms/step, {total / sec / 1e6:.2f} M tokens/s")
+    out = {
+        "metric": f"fwd+bwd tokens/s, {w.B} packed sequences of lengths in [{w.T // 4}, {w.T}], attn block bf16 "
+                  f"C{C} H{H} N{N}",
+        "value": round(total / sec, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": w.name, "sequences": w.B, "tokens_per_step": total, "max_len": L, "C": C, "H": H,
+                   "N": N, "parallelism": "single-gpu"},
+        "peak_hbm": {"fused_bytes": int(peak)},
+        "block_tflops": round(flops / sec / 1e12, 2),
         "roofline": roofline_of(prof, work),
         "kernels": kernels,
         "cpu_baseline": None,
