@@ -125,8 +125,8 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 //   dQ^T += K^T dS^T
 // whose A operand K^T is read from the row-major K tile with the transposing
 // ds_read_b64_tr_b16. Key tiles of 64 stream through LDS (global_load_lds,
-// double-buffered, one barrier per tile); tiles below the workgroup's first
-// query run in a branch-free loop, the diagonal region after it.
+// double-buffered, one barrier per tile); tiles wholly below a wave's first
+// query run in a branch-free loop, the rest of the diagonal region after it.
 // ---------------------------------------------------------------------------
 template <int N, bool VARLEN>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
@@ -301,7 +301,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   };
 
   const int nkv = (kv_end + BKV - 1) / BKV;
-  const int nfull = min(nkv, (qi * BQ) / BKV);
+  // Branch-free loop over the tiles wholly below this wave's first query and
+  // inside the sequence; the split point is per wave (one barrier per tile
+  // in either loop keeps the waves in step).
+  const int nfull = min(nkv, min(q0w + 1, T) / BKV);
   issue_tile(0, 0);
   wait_vmcnt0();  // also retires the q/dO fragment loads
   __syncthreads();

@@ -342,12 +342,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     PV(1, 1);
   };
 
-  // Tiles below the workgroup's first query need no mask for any wave and
-  // run in a branch-free loop; the (at most four) tiles of the diagonal
-  // region, and a ragged sequence end, follow in a second loop.
+  // Tiles wholly below a wave's first query (and inside the sequence) need
+  // no mask for that wave and run in a branch-free loop; the rest of the
+  // diagonal region and a ragged sequence end follow in a second loop. The
+  // split point is per wave: every wave still passes one barrier per tile,
+  // so the two loops together keep the waves in step.
   auto main_loop = [&](auto fixed_tag) {
     const int nkv = (kv_end + BKV - 1) / BKV;
-    const int nfull = min(nkv, (qi * BQ) / BKV);
+    const int nfull = min(nkv, min(q0w + 1, T) / BKV);
     issue_tile(0, 0);
     wait_vmcnt0();  // also retires the Q fragment loads
     __syncthreads();
