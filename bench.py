@@ -165,6 +165,7 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="time KV-cache decode steps (one token per sequence) instead of fwd+bwd")
     ap.add_argument("--context", type=int, default=None, help="decode: cached tokens per sequence (default T - 1)")
+    ap.add_argument("--graph", action="store_true", help="decode: also time the step replayed from a captured graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 256 MiB five times (reference for HBM byte counters)")
     args = ap.parse_args()
@@ -479,7 +480,7 @@ def decode_bench(args, w):
     import torch
 
     from memory_efficient_attn_layer_amd import _lib
-    from memory_efficient_attn_layer_amd.decode import KVCache, decode_step, prefill
+    from memory_efficient_attn_layer_amd.decode import DecodeGraph, KVCache, decode_step, prefill
     from memory_efficient_attn_layer_amd.synthetic import make_inputs
 
     L = w.T - 1 if args.context is None else int(args.context)
@@ -523,6 +524,11 @@ def decode_bench(args, w):
     dec_ms = prof["attn_decode"][1] / prof["attn_decode"][0]
     achieved = kv_bytes / (dec_ms * 1e-3) / 1e9
     log(f"{sec * 1e6:.1f} us/step, {B / sec:.0f} tokens/s; cache read {achieved:.0f} GB/s")
+    eager_sec = sec
+    if args.graph:
+        graph = DecodeGraph(*wts, f1, f2, H, N, cache)
+        sec = measure(lambda: graph.step(xt, pos), steps, 5, sync)
+        log(f"graph replay: {sec * 1e6:.1f} us/step, {B / sec:.0f} tokens/s")
     out = {
         "metric": f"decode tokens/s (one token per sequence per step) at context {L}, attn block bf16 "
                   f"B{B} C{C} H{H} N{N}",
@@ -541,6 +547,8 @@ def decode_bench(args, w):
                    "cache_bytes_read_per_step": int(kv_bytes), "weight_bytes_per_step": int(w_bytes),
                    "parallelism": "single-gpu"},
         "step_hbm_gbs": round((kv_bytes + w_bytes) / sec / 1e9, 1),
+        "graph": bool(args.graph),
+        "eager_ms_per_step": round(eager_sec * 1e3, 5),
         "peak_hbm": {"step_bytes": int(peak)},
         "roofline": {"kernel": "attn_decode", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),

@@ -5,7 +5,7 @@ xTimeCrystal/memory_efficient_attn_layer (fast_triton_attn.py:373-697), backed
 by hand-written HIP kernels in libmea.so (C ABI: include/mea.h).
 """
 from .attention import FusedAttentionFunction, FusedAttentionVarlenFunction, fused_attn, fused_attn_varlen
-from .decode import KVCache, decode_step, prefill
+from .decode import DecodeGraph, KVCache, decode_step, prefill
 from .module import CausalSoftmaxAttention
 from .yarn import Yarn, rotary_tables, swap_even_odd
 
@@ -16,6 +16,7 @@ __all__ = [
     "fused_attn_varlen",
     "CausalSoftmaxAttention",
     "KVCache",
+    "DecodeGraph",
     "prefill",
     "decode_step",
     "Yarn",

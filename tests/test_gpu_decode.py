@@ -118,3 +118,30 @@ def test_decode_matches_prefill_rows():
     for t in (0, 1, 150, 299):
         y = blk.decode(x[:, t], [t] * B, cache)
         assert_out_close(f"t{t}", y, y_pre[:, t])
+
+
+def test_decode_graph_replays_match_eager_steps():
+    # Captured decode steps, replayed several times with eager work and
+    # synchronisation between the replays; every replay must equal the eager
+    # step on the same inputs bitwise (same kernels, same cache contents).
+    from memory_efficient_attn_layer_amd.decode import DecodeGraph
+
+    C, H, N, B, T0, cap = 512, 4, 128, 3, 100, 160
+    ws, f1, f2, g = _params(C, H, N, cap, seed=13)
+    blk = _Block(ws, f1, f2, H, N)
+    x = torch.randn(B, T0 + 6, C, generator=g).bfloat16()
+    cache_e = KVCache.empty(B, H, N, cap, "cuda")
+    cache_g = KVCache.empty(B, H, N, cap, "cuda")
+    blk.prefill(x[:, :T0], cache_e)
+    blk.prefill(x[:, :T0], cache_g)
+    graph = DecodeGraph(*blk.ws, blk.f1, blk.f2, H, N, cache_g)
+    # The warm-up and capture wrote row 0 of the graph's cache: restore it.
+    blk.prefill(x[:, :T0], cache_g)
+    for s in range(6):
+        pos = [T0 + s, T0 + s, max(0, T0 - 40 + 7 * s)]
+        y_e = blk.decode(x[:, T0 + s], pos, cache_e)
+        y_g = graph.step(x[:, T0 + s].cuda(), torch.tensor(pos, dtype=torch.int32, device="cuda")).clone()
+        torch.cuda.synchronize()
+        _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # eager work between replays
+        assert torch.equal(y_g, y_e), f"replay {s}"
+        assert torch.equal(cache_g.k, cache_e.k) and torch.equal(cache_g.v, cache_e.v), f"cache after replay {s}"
