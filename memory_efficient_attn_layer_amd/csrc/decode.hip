@@ -66,11 +66,18 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void attn_decode_kernel(DecodePa
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
 
   for (int k0 = k_begin; k0 < k_end; k0 += KB) {
-    u32x4 kr[NI];
+    // The block's K and V rows are requested together (V does not depend on
+    // the scores), so twice the bytes are in flight per wave.
+    u32x4 kr[NI], vr[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + i * KPI + j;
       kr[i] = key < k_end ? ld16(kc + (size_t)key * N) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int key = k0 + i * KPI + j;
+      vr[i] = key < k_end ? ld16(vc + (size_t)key * N) : u32x4{0u, 0u, 0u, 0u};
     }
     float sc[NI];
 #pragma unroll
@@ -96,12 +103,6 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void attn_decode_kernel(DecodePa
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] *= alpha;
     m_run = m_new;
-    u32x4 vr[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int key = k0 + i * KPI + j;
-      vr[i] = key < k_end ? ld16(vc + (size_t)key * N) : u32x4{0u, 0u, 0u, 0u};
-    }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const float pv = exp2f(sc[i] - m_new);  // 0 for keys past the split
