@@ -41,71 +41,94 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
                                              const bf16_bits* xrot, float xscale, const float* rstat,
                                              bf16_bits* out) {
   constexpr int CPR = N / 8, RPP = 64 / CPR;
+  constexpr int NP = 32 / RPP, PB = 2;  // passes; passes whose global operands are fetched together
+  static_assert(NP % PB == 0, "pass batches");
   const int lane = threadIdx.x & 63;
   const size_t ld = (size_t)p.ld_da;
 #pragma unroll 1
-  for (int pass = 0; pass < 32 / RPP; ++pass) {
-    const int row = pass * RPP + lane / CPR, dc = lane % CPR;
-    const int t = t0 + row;
-    const bool valid = t < T;
-    const int tc = valid ? t : T - 1;
-    float dv[8];
-    {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(stg + row * FP + dc * 8);
-      const f32x4 c = *reinterpret_cast<const f32x4*>(stg + row * FP + dc * 8 + 4);
+  for (int p0 = 0; p0 < NP; p0 += PB) {
+    // Every global operand of the batch's rows is requested first: one
+    // memory round trip per batch instead of one per pass.
+    u32x4 xw[PB];
+    f32x4 f1w[PB][2], f2w[PB][2];
+    float rxw[PB], rrw[PB];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { dv[i] = a[i]; dv[4 + i] = c[i]; }
+    for (int k = 0; k < PB; ++k) {
+      const int row = (p0 + k) * RPP + lane / CPR, dc = lane % CPR;
+      const int t = t0 + row, tc = t < T ? t : T - 1;
+      rxw[k] = p.rx[tok_row0 + tc];
+      if (rotary) {
+        xw[k] = ld16(xrot + (head_row0 + tc) * N + dc * 8);
+        const float* f1r = p.f1 + (size_t)tc * N + dc * 8;
+        const float* f2r = p.f2 + (size_t)tc * N + dc * 8;
+        f1w[k][0] = *reinterpret_cast<const f32x4*>(f1r);
+        f1w[k][1] = *reinterpret_cast<const f32x4*>(f1r + 4);
+        f2w[k][0] = *reinterpret_cast<const f32x4*>(f2r);
+        f2w[k][1] = *reinterpret_cast<const f32x4*>(f2r + 4);
+        rrw[k] = rstat[head_row0 + tc];
+      }
     }
-    const float rxv = p.rx[tok_row0 + tc];
-    float res[8];
-    if (rotary) {
-      float xv[8], a1[8], a2[8];
-      unpack8(ld16(xrot + (head_row0 + tc) * N + dc * 8), xv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xv[i] *= xscale;
-      const float* f1r = p.f1 + (size_t)tc * N + dc * 8;
-      const float* f2r = p.f2 + (size_t)tc * N + dc * 8;
+    for (int k = 0; k < PB; ++k) {
+      const int row = (p0 + k) * RPP + lane / CPR, dc = lane % CPR;
+      const int t = t0 + row;
+      const bool valid = t < T;
+      float dv[8];
+      {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(stg + row * FP + dc * 8);
+        const f32x4 c = *reinterpret_cast<const f32x4*>(stg + row * FP + dc * 8 + 4);
 #pragma unroll
-      for (int i = 0; i < 8; i += 4) {
-        const f32x4 u = *reinterpret_cast<const f32x4*>(f1r + i);
-        const f32x4 w = *reinterpret_cast<const f32x4*>(f2r + i);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { a1[i + e] = u[e]; a2[i + e] = w[e]; }
+        for (int i = 0; i < 4; ++i) { dv[i] = a[i]; dv[4 + i] = c[i]; }
       }
-      float xh[8], dh[8], dot = 0.f;
+      const float rxv = rxw[k];
+      float res[8];
+      if (rotary) {
+        float xv[8], a1[8], a2[8];
+        unpack8(xw[k], xv);
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        const float det = a1[i] * a1[i + 1] - a2[i] * a2[i + 1];
-        const float inv = 1.0f / det;
-        xh[i] = (a1[i + 1] * xv[i] - a2[i] * xv[i + 1]) * inv;
-        xh[i + 1] = (a1[i] * xv[i + 1] - a2[i + 1] * xv[i]) * inv;
-        dh[i] = a1[i] * dv[i] + a2[i + 1] * dv[i + 1];
-        dh[i + 1] = a1[i + 1] * dv[i + 1] + a2[i] * dv[i];
-        dot += dh[i] * xh[i] + dh[i + 1] * xh[i + 1];
-      }
-      // Reduce the dot product over the CPR lanes of this row.
-      dot += xor1(dot);
-      dot += xor2(dot);
-      dot += shfl_xor(dot, 4);
-      if (CPR == 16) dot += shfl_xor(dot, 8);
-      const float rr = rstat[head_row0 + tc];
-      const float sc = rxv * rr, cf = dot / (float)N;
+        for (int i = 0; i < 8; ++i) xv[i] *= xscale;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) res[i] = sc * (dh[i] - xh[i] * cf);
-      if (p.df1 != nullptr && valid) {
-        float* d1 = p.df1 + (size_t)t * N + dc * 8;
-        float* d2 = p.df2 + (size_t)t * N + dc * 8;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          atomicAdd(d1 + i, dv[i] * xh[i]);
-          atomicAdd(d2 + i, dv[i] * xh[i ^ 1]);
+        for (int e = 0; e < 4; ++e) {
+          a1[e] = f1w[k][0][e];
+          a1[4 + e] = f1w[k][1][e];
+          a2[e] = f2w[k][0][e];
+          a2[4 + e] = f2w[k][1][e];
         }
-      }
-    } else {
+        float xh[8], dh[8], dot = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) res[i] = rxv * dv[i];
+        for (int i = 0; i < 8; i += 2) {
+          const float det = a1[i] * a1[i + 1] - a2[i] * a2[i + 1];
+          const float inv = 1.0f / det;
+          xh[i] = (a1[i + 1] * xv[i] - a2[i] * xv[i + 1]) * inv;
+          xh[i + 1] = (a1[i] * xv[i + 1] - a2[i + 1] * xv[i]) * inv;
+          dh[i] = a1[i] * dv[i] + a2[i + 1] * dv[i + 1];
+          dh[i + 1] = a1[i + 1] * dv[i + 1] + a2[i] * dv[i];
+          dot += dh[i] * xh[i] + dh[i + 1] * xh[i + 1];
+        }
+        // Reduce the dot product over the CPR lanes of this row.
+        dot += xor1(dot);
+        dot += xor2(dot);
+        dot += shfl_xor(dot, 4);
+        if (CPR == 16) dot += shfl_xor(dot, 8);
+        const float rr = rrw[k];
+        const float sc = rxv * rr, cf = dot / (float)N;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) res[i] = sc * (dh[i] - xh[i] * cf);
+        if (p.df1 != nullptr && valid) {
+          float* d1 = p.df1 + (size_t)t * N + dc * 8;
+          float* d2 = p.df2 + (size_t)t * N + dc * 8;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            atomicAdd(d1 + i, dv[i] * xh[i]);
+            atomicAdd(d2 + i, dv[i] * xh[i ^ 1]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) res[i] = rxv * dv[i];
+      }
+      if (valid) st16(out + (tok_row0 + t) * ld + (size_t)h * N + dc * 8, pack8(res));
     }
-    if (valid) st16(out + (tok_row0 + t) * ld + (size_t)h * N + dc * 8, pack8(res));
   }
 }
 

@@ -102,6 +102,22 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzPara
   float* stg = reinterpret_cast<float*>(smem) + wave * 16 * FP;  // the main loop ended on a barrier
 #pragma unroll
   for (int tb = 0; tb < S::TB; ++tb) {
+    // The block's sigmoid(a_g), O and rx rows are requested before its
+    // staging, so one memory round trip serves all four row groups (a load
+    // issued after this block's stores would also wait for them).
+    u32x4 sgw[4], ovw[4];
+    float rxw[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int row = it * 4 + (lane >> 4), cc = lane & 15;
+      const int m = m0 + wt * 64 + tb * 16 + row;
+      const int j = f0 + wf * 128 + cc * 8;
+      const int mc = m < M ? m : M - 1, jc = j < HN ? j : 0;
+      const size_t off = (size_t)mc * HN + jc;
+      sgw[it] = ld16(p.sig + off);
+      ovw[it] = ld16(p.o + off);
+      rxw[it] = p.rx[mc];
+    }
 #pragma unroll
     for (int fb = 0; fb < S::FB; ++fb)
       *reinterpret_cast<f32x4*>(stg + c16 * FP + 16 * fb + 4 * g) = acc[fb][tb];
@@ -121,9 +137,9 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzPara
         for (int i = 0; i < 4; ++i) { dz[i] = a[i]; dz[4 + i] = c[i]; }
       }
       const size_t off = (size_t)mc * HN + jc;
-      unpack8(ld16(p.sig + off), sg);
-      unpack8(ld16(p.o + off), ov);
-      const float rxv = p.rx[mc];
+      unpack8(sgw[it], sg);
+      unpack8(ovw[it], ov);
+      const float rxv = rxw[it];
       float dov[8], dag[8], zv[8], dl = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
