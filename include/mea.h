@@ -61,7 +61,8 @@ enum {
   MEA_ERR_WORKSPACE = -5,   /* workspace smaller than mea_workspace_bytes() */
   MEA_ERR_ALIGN = -6,       /* a pointer is not 16-byte aligned */
   MEA_ERR_EPS = -7,         /* eps not finite and positive */
-  MEA_ERR_LAUNCH = -8       /* HIP reported an error at launch */
+  MEA_ERR_LAUNCH = -8,      /* HIP reported an error at launch */
+  MEA_ERR_ALIAS = -9        /* dx overlaps another argument of mea_bwd */
 };
 
 /* Which pass a workspace size is asked for. */
@@ -109,6 +110,10 @@ int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk,
  *   dwo                 (C, H*N) bf16      out
  *   df1, df2            (T_max, N) fp32    out, rows 0..T-1 written; both may
  *                                          be NULL to skip the table gradient
+ *
+ * dx also holds the gradient of the gate projection's output (rows of H*N
+ * values at stride C) until the last kernel overwrites it with the result,
+ * when H*N <= C; it must not overlap any other argument (MEA_ERR_ALIAS).
  */
 int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq,
             const void* wk, const void* wv, const void* wg, const void* wo,

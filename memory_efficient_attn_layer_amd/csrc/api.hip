@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "../../include/mea.h"
@@ -19,7 +20,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // Byte offsets of every transient inside the workspace.
 struct Layout {
   size_t q, k, v, sig, tpos, o, qkn;         // forward (tpos: packed sequences only)
-  size_t dO, da;                             // backward; da = [da_q|da_k|da_v|da_g] (M, 4HN)
+  size_t dO, daq, dag;                       // backward (da_k, da_v overwrite k, v)
   size_t rx, rq, rk, delta, woT, wcatT, part;
   size_t total;
 };
@@ -40,7 +41,9 @@ Layout make_layout(const mea_desc& d, int pass) {
     L.qkn = take(2 * sizeof(float));
   } else {
     L.dO = take(act);
-    L.da = take(4 * M * HN * 2);
+    L.daq = take(act);
+    // da_g lives in the caller's dx buffer when its rows fit (HN <= C).
+    L.dag = HN <= C ? 0 : take(act);
     L.rx = take(M * 4);
     L.rq = take(stat);
     L.rk = take(stat);
@@ -66,6 +69,9 @@ int validate(const mea_desc* d, int pass) {
   if (M >= (INT64_C(1) << 31) || HN >= 65536 || d->B * d->H * d->T >= (INT64_C(1) << 31) ||
       d->T_max * d->N >= (INT64_C(1) << 31))
     return MEA_ERR_SHAPE;
+  // The backward GEMMs address a head-major gradient with 32-bit byte
+  // offsets spanning up to one head of one batch plus a few hundred rows.
+  if (pass == MEA_PASS_BWD && d->H * (d->T + 256) * d->N >= (INT64_C(1) << 30)) return MEA_ERR_SHAPE;
   return MEA_OK;
 }
 
@@ -93,6 +99,13 @@ int validate_pass(const mea_desc* d, int pass, const Varlen* var) {
   if (var->cu == nullptr) return MEA_ERR_NULL;
   if (((uintptr_t)var->cu & 3u) != 0) return MEA_ERR_ALIGN;
   return MEA_OK;
+}
+
+// Whether byte ranges [a, a + na) and [b, b + nb) overlap (null b: no).
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  if (b == nullptr) return false;
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + nb && y < x + na;
 }
 
 int check_ptrs(std::initializer_list<const void*> ps) {
@@ -346,6 +359,19 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
   if (rc != MEA_OK) return rc;
   if ((df1 == nullptr) != (df2 == nullptr)) return MEA_ERR_NULL;
   if (df1 != nullptr && (!aligned16(df1) || !aligned16(df2))) return MEA_ERR_ALIGN;
+  {
+    // dx is written before the end (it holds da_g while HN <= C): it may
+    // overlap nothing else.
+    const size_t M = (size_t)(d->B * d->T), HN = (size_t)(d->H * d->N), C = (size_t)d->C;
+    const size_t act_c = M * C * 2, wbytes = HN * C * 2, tbytes = (size_t)d->T_max * (size_t)d->N * 4;
+    const std::pair<const void*, size_t> others[] = {
+        {dy, act_c},  {x, act_c},   {wq, wbytes},  {wk, wbytes},  {wv, wbytes},  {wg, wbytes},
+        {wo, wbytes}, {f1, tbytes}, {f2, tbytes},  {o_save, M * HN * 2},       {lse_save, M * (size_t)d->H * 4},
+        {dwq, wbytes}, {dwk, wbytes}, {dwv, wbytes}, {dwg, wbytes}, {dwo, wbytes}, {df1, tbytes},
+        {df2, tbytes}, {ws, ws_bytes}};
+    for (const auto& o : others)
+      if (overlaps(dx, act_c, o.first, o.second)) return MEA_ERR_ALIAS;
+  }
   const Layout L = make_layout(*d, MEA_PASS_BWD);
   if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -357,11 +383,16 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
   bf16_bits* v = at<bf16_bits>(ws, L.v);
   bf16_bits* sig = at<bf16_bits>(ws, L.sig);
   bf16_bits* dO = at<bf16_bits>(ws, L.dO);
-  bf16_bits* da = at<bf16_bits>(ws, L.da);  // row stride 4 HN
-  bf16_bits* daq = da;
-  bf16_bits* dak = da + HN;
-  bf16_bits* dav = da + 2 * HN;
-  bf16_bits* dag = da + 3 * HN;
+  // Gradients of the projection outputs: da_q, and da_k / da_v written over
+  // k / v by the dK/dV kernel (the last reader of k and v), head-major;
+  // da_g token-major, in the rows of dx when they are wide enough (each dx
+  // workgroup reads the da_g rows it later overwrites, and nothing else
+  // reads them after the weight gradients).
+  bf16_bits* daq = at<bf16_bits>(ws, L.daq);
+  const bool dag_in_dx = HN <= C;
+  bf16_bits* dag = dag_in_dx ? static_cast<bf16_bits*>(dx) : at<bf16_bits>(ws, L.dag);
+  const int ld_dag = dag_in_dx ? C : HN;
+  const mea::DaParts da = {daq, k, v, dag, ld_dag, (int)d->B, T, H, N};
   float* rx = at<float>(ws, L.rx);
   float* rq = at<float>(ws, L.rq);
   float* rk = at<float>(ws, L.rk);
@@ -408,7 +439,7 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
   dz.C = C;
   dz.H = H;
   dz.N = N;
-  dz.ld_da = 4 * HN;
+  dz.ld_dag = ld_dag;
   MEA_TRY(timed(K_DZ_GATE_BWD, s, [&] { return mea::launch_dz_gate_bwd(dz, s); }));
 
   mea::AttnBwdParams ab;
@@ -424,14 +455,13 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
   ab.rq = rq;
   ab.rk = rk;
   ab.daq = daq;
-  ab.dak = dak;
-  ab.dav = dav;
+  ab.dak = k;
+  ab.dav = v;
   ab.df1 = df1;
   ab.df2 = df2;
   ab.B = (int)d->B;
   ab.H = H;
   ab.T = T;
-  ab.ld_da = 4 * HN;
   ab.scale = (float)(1.0 / sqrt((double)N));
   ab.sl2e = 1.0f;  // q was stored in log2 units by the recompute above
   ab.qscale = qs;
@@ -670,6 +700,7 @@ const char* mea_strerror(int code) {
     case MEA_ERR_ALIGN: return "a pointer is not 16-byte aligned";
     case MEA_ERR_EPS: return "eps must be finite and positive";
     case MEA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case MEA_ERR_ALIAS: return "dx overlaps another argument of the backward";
     default: return "unknown status";
   }
 }

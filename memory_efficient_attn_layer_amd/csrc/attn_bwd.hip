@@ -34,17 +34,19 @@ namespace mea {
 //   rotary != 0 : head RMSNorm + rotary backward of q or k (xrot = q or k
 //                 as stored, xrot * xscale the rotated rows themselves).
 //   rotary == 0 : plain copy (v).
-// Output row t goes to out[(b*T + t)*ld_da + h*N ...], scaled by rx[b*T + t].
+// Output row t goes to out[(head_row0 + t)*N ...] (head-major, like q, k, v),
+// scaled by rx[tok_row0 + t]. out may be xrot itself: every lane writes only
+// the 16 bytes it has read, after reading them, and rows past T are not
+// written.
 template <int N>
 __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, const AttnBwdParams& p, int T,
-                                             size_t tok_row0, size_t head_row0, int h, bool rotary,
+                                             size_t tok_row0, size_t head_row0, bool rotary,
                                              const bf16_bits* xrot, float xscale, const float* rstat,
                                              bf16_bits* out) {
   constexpr int CPR = N / 8, RPP = 64 / CPR;
   constexpr int NP = 32 / RPP, PB = 2;  // passes; passes whose global operands are fetched together
   static_assert(NP % PB == 0, "pass batches");
   const int lane = threadIdx.x & 63;
-  const size_t ld = (size_t)p.ld_da;
 #pragma unroll 1
   for (int p0 = 0; p0 < NP; p0 += PB) {
     // Every global operand of the batch's rows is requested first: one
@@ -127,7 +129,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 #pragma unroll
         for (int i = 0; i < 8; ++i) res[i] = rxv * dv[i];
       }
-      if (valid) st16(out + (tok_row0 + t) * ld + (size_t)h * N + dc * 8, pack8(res));
+      if (valid) st16(out + (head_row0 + t) * N + dc * 8, pack8(res));
     }
   }
 }
@@ -367,7 +369,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   __syncthreads();
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb)
-    head_row_bwd<N>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, T, tok_row0, head_row0, hd, true, p.q,
+    head_row_bwd<N>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, T, tok_row0, head_row0, true, p.q,
                     1.0f / p.qscale, p.rq, p.daq);
 }
 
@@ -632,7 +634,7 @@ __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(Att
         *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v;
       }
     __syncthreads();
-    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, hd, false, nullptr, 1.0f, nullptr, p.dav);
+    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, false, nullptr, 1.0f, nullptr, p.dav);
     __syncthreads();
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -642,7 +644,7 @@ __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(Att
         *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v * (p.scale / p.qscale);
       }
     __syncthreads();
-    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, hd, true, p.k, 1.0f, p.rk, p.dak);
+    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, true, p.k, 1.0f, p.rk, p.dak);
     __syncthreads();
   }
 }

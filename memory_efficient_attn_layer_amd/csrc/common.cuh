@@ -71,6 +71,12 @@ __device__ __forceinline__ void g2lds16(const void* gsrc, bf16_bits* lds_wave_ba
   const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)((lds_void*)lds_wave_base));
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gsrc), "s"(lds) : "memory");
 }
+// The same, into the LDS byte address lds (wave-uniform).
+__device__ __forceinline__ void g2lds16(const void* gsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gsrc),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
 // The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit
 // per-lane byte offset (saddr form), into the LDS byte address lds (also
 // wave-uniform). Saves the per-lane 64-bit address arithmetic.

@@ -159,7 +159,7 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzPara
         const int b = mc / T, t = mc - b * T;
         const size_t hrow = ((size_t)b * H + hh) * T + t;
         st16(p.dO + hrow * N + n, pack8(dov));
-        st16(p.dag + (size_t)mc * p.ld_da + jc, pack8(dag));
+        st16(p.dag + (size_t)mc * p.ld_dag + jc, pack8(dag));
         st16(p.sig + off, pack8(zv));  // sigmoid(a_g) is dead from here on
         if (n == 0) p.delta[hrow] = dl;
       }
@@ -186,13 +186,24 @@ hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Part `part` of da as a pointer, without branches or an indexed read (a
+// pointer picked by index from the parameters is read from a private copy).
+__device__ __forceinline__ const bf16_bits* da_part(const DaParts& dp, int part) {
+  auto m = [&](const bf16_bits* ptr, int i) { return (uint64_t)(uintptr_t)ptr & (0ull - (uint64_t)(part == i)); };
+  return reinterpret_cast<const bf16_bits*>((uintptr_t)(m(dp.q, 0) | m(dp.k, 1) | m(dp.v, 2) | m(dp.g, 3)));
+}
+
 // ---------------------------------------------------------------------------
 // dx = rmsnorm_bwd([da_q|da_k|da_v|da_g] Wcat), one workgroup owns full rows.
 //
 // Computed transposed, D^T = Wcat^T da^T: A = Wcat^T rows (C features, k =
-// 4HN contiguous), B = da rows (tokens). A workgroup covers all C features of
-// BT tokens with WF x WT waves of 128 features x 64 tokens; k-slabs of 32
-// stream through a 3-stage LDS ring filled by direct global->LDS loads. In
+// 4HN contiguous), B = da rows (tokens). A 32-wide k-slab of da lies in one
+// head of one part (N >= 64): each slab has one base address, and a lane's
+// row offset from it, the same in every slab, is precomputed for the
+// head-major parts (q, k, v) and for the token-major da_g. A workgroup
+// covers all C features of BT tokens with WF x WT waves of 128 features x 64
+// tokens; k-slabs of 32 stream through a 3-stage LDS ring filled by direct
+// global->LDS loads. In
 // the accumulator layout a lane holds one token and 4 consecutive features,
 // so the RMSNorm backward dot (acc . x) is an in-lane sum, two lane
 // exchanges and a cross-wave sum through LDS; dx rows leave through an LDS
@@ -220,18 +231,52 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wf = wave % WF, wt = wave / WF;
   const bf16_bits* wt_g = p.wcatT;  // (C, 4HN)
-  const bf16_bits* da = p.da;       // (M, 4HN)
+  const DaParts& dp = p.da;
+  const int HN = p.HN, N = dp.N, T = dp.T;
 
+  // Token rows of the da slabs: group u of load instructions starts at token
+  // mf(u); hm(m) is token m's row in a head-major array, in units of N from
+  // head 0 of batch 0.
+  using Plan = SlabPlan<BT, NW, BK>;
+  auto mf = [&](int u) { return min(m0 + u * NW * 16, M - 1); };
+  auto hm = [&](int m) { return (m / T) * (dp.H - 1) * T + m; };
+  Plan plan_t, plan_h;
+  slab_plan(plan_t, wave, dp.ld_g, [&](int u, int i) { return min(m0 + u * NW * 16 + i, M - 1) - mf(u); });
+  slab_plan(plan_h, wave, N, [&](int u, int i) { return hm(min(m0 + u * NW * 16 + i, M - 1)) - hm(mf(u)); });
+  int hmf[Plan::NU];
+#pragma unroll
+  for (int u = 0; u < Plan::NU; ++u) hmf[u] = __builtin_amdgcn_readfirstlane(hm(mf(u)));
+
+  // Slabs are issued in order ks = 0, 1, 2, ...; (part, hh, n0) locate the
+  // next one: part of da, head, first column within the head.
+  int part = 0, hh = 0, n0 = 0;
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int ks, int st) {
     const uint32_t lds = lds0 + (uint32_t)(st * STAGE) * 2u;
     const int k0 = ks * BK;
     slab_issue<C, NW, BK>(
         lds, wave, K4, [&](int u) { return wt_g + (size_t)(u * NW * 16) * K4 + k0; }, [](int, int i) { return i; });
-    slab_issue<BT, NW, BK>(
-        lds + C * BK * 2, wave, K4,
-        [&](int u) { return da + (size_t)min(m0 + u * NW * 16, M - 1) * K4 + k0; },
-        [&](int u, int i) { return min(m0 + u * NW * 16 + i, M - 1) - min(m0 + u * NW * 16, M - 1); });
+    {
+      const bool tokm = part == 3;
+      const bf16_bits* src = da_part(dp, part);
+      constexpr int NU = Plan::NU, NI = Plan::NI;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int ins = u * NW + wave;
+        if (NI % NW != 0 && ins >= NI) break;  // wave-uniform: partial last round
+        const size_t off = tokm ? (size_t)mf(u) * dp.ld_g + (hh * N + n0) : ((size_t)hh * T + hmf[u]) * N + n0;
+        g2lds16_s(src + off, tokm ? plan_t.voff[u] : plan_h.voff[u],
+                  lds + (uint32_t)(C * BK * 2) + (uint32_t)ins * 1024u);
+      }
+    }
+    n0 += BK;
+    if (n0 == N) {
+      n0 = 0;
+      if (++hh == dp.H) {
+        hh = 0;
+        ++part;
+      }
+    }
   };
 
   f32x4 acc[FB][TB];
@@ -374,6 +419,51 @@ __device__ __forceinline__ void dw_issue(uint32_t lds, int wave, const bf16_bits
   }
 }
 
+// The A slabs of problem 0 read da, whose parts have two layouts (da_q,
+// da_k, da_v head-major, da_g token-major). A lane's column is the same in
+// every slab and its token row advances by kDwBK per slab, so each lane
+// keeps a cursor: the column's address in row 0 and the row's batch. In a
+// head-major part token m = b*T + t sits at row b*H*T + t = m + b*(H-1)*T
+// (in units of N from the column's head in batch 0).
+struct DaCursor {
+  const bf16_bits* col;  // part + the lane's column offset
+  int rstride;           // elements per row: N, or ld_g for da_g
+  int bstep;             // (H-1)*T, or 0 for da_g
+  int m, b, nb;          // token row, its batch, first token of batch b+1
+  int last;              // row of token M-1
+};
+
+__device__ __forceinline__ void da_cursor_init(DaCursor& c, const DaParts& dp, int HN, int feature, int m, int M) {
+  const int part = feature / HN, f = feature - part * HN;
+  if (part == 3) {
+    c.col = dp.g + f;
+    c.rstride = dp.ld_g;
+    c.bstep = 0;
+  } else {
+    const bf16_bits* src = part == 0 ? dp.q : part == 1 ? dp.k : dp.v;
+    const int hh = f / dp.N;
+    c.col = src + (size_t)hh * dp.T * dp.N + (f - hh * dp.N);
+    c.rstride = dp.N;
+    c.bstep = (dp.H - 1) * dp.T;
+  }
+  c.m = m;
+  c.b = m / dp.T;
+  c.nb = (c.b + 1) * dp.T;
+  c.last = (M - 1) + ((M - 1) / dp.T) * c.bstep;
+}
+
+// Address of the cursor's current row (rows past M - 1 read row M - 1),
+// then one slab further.
+__device__ __forceinline__ const bf16_bits* da_cursor_next(DaCursor& c, int T, int M) {
+  while (c.m >= c.nb) {
+    ++c.b;
+    c.nb += T;
+  }
+  const int row = c.m < M ? c.m + c.b * c.bstep : c.last;
+  c.m += kDwBK;
+  return c.col + (size_t)row * c.rstride;
+}
+
 // MFMA operand of feature block f (16 features) from a slab: lane (g, c16)
 // gets feature 16 f + c16 of tokens 8g .. 8g+7.
 __device__ __forceinline__ bf16x8 dw_frag(const bf16_bits* slab, int f, int lane) {
@@ -388,6 +478,7 @@ __device__ __forceinline__ bf16x8 dw_frag(const bf16_bits* slab, int f, int lane
 
 }  // namespace
 
+template <bool FAST>
 __global__ __launch_bounds__(512, 1) void dw_partial_kernel(DwParams p) {
   constexpr int STAGES = 3;
   __shared__ __attribute__((aligned(16))) bf16_bits smem[STAGES * 2 * kDwSlab];
@@ -404,9 +495,8 @@ __global__ __launch_bounds__(512, 1) void dw_partial_kernel(DwParams p) {
   const int ntj = prob1 ? (HN + kDwTile - 1) / kDwTile : C / kDwTile;
   const int i0 = (lt / ntj) * kDwTile, j0 = (lt % ntj) * kDwTile;
   const int I = prob1 ? C : K4, J = prob1 ? HN : C;
-  const bf16_bits* asrc = prob1 ? p.dy : p.da;
   const bf16_bits* bsrc = prob1 ? p.z : p.x;
-  const int lda = prob1 ? C : K4, ldb = prob1 ? HN : C;
+  const int ldb = prob1 ? HN : C;
 
   const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -416,12 +506,67 @@ __global__ __launch_bounds__(512, 1) void dw_partial_kernel(DwParams p) {
   const int mbeg = z * chunk, mend = min(M, mbeg + chunk);
   const int ns = mbeg < mend ? (mend - mbeg + kDwBK - 1) / kDwBK : 0;
 
+  // A slabs (this lane: rows 2 * ins + lane / 32, ins = 8u + wave; column
+  // chunk as in dw_issue). Slabs are issued in order s = 0, 1, 2, ...
+  //  FAST (T a multiple of kDwBK, HN of kDwTile; then every token chunk is a
+  //  multiple of kDwBK): no slab crosses a sequence or runs past M and the
+  //  tile's columns lie in one part, so slab s reads from the uniform base
+  //  asrc + arow * ald, arow being the row of its first token (head-major
+  //  parts: b*H*T + t; token-major sources: m), at a per-lane offset that is
+  //  the same in every slab. Each issue advances arow (and stt, the first
+  //  token's position in its sequence, to step arow over the other heads).
+  //  Otherwise problem 0 follows every lane's row with a cursor.
+  const DaParts& dp = p.da;
+  const bf16_bits* asrc = nullptr;
+  int ald = 0, bstep = 0, arow = 0, stt = 0;
+  uint32_t avoff[2] = {0u, 0u};
+  DaCursor cur[2];
+  if (FAST) {
+    const int apart = prob1 ? 4 : i0 / HN;
+    const bool hmaj = apart < 3;
+    asrc = prob1 ? p.dy : da_part(dp, apart);
+    ald = prob1 ? C : hmaj ? dp.N : dp.ld_g;
+    bstep = hmaj ? (dp.H - 1) * dp.T : 0;
+    const int sb = mbeg / dp.T;
+    stt = mbeg - sb * dp.T;
+    arow = hmaj ? sb * dp.H * dp.T + stt : mbeg;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = 2 * (u * 8 + wave) + (lane >> 5);
+      const int f = i0 - (prob1 ? 0 : apart * HN) + 8 * ((lane & 31) ^ dw_swz(row));
+      const int hh = f / dp.N;
+      avoff[u] = (uint32_t)(hmaj ? (hh * dp.T + row) * dp.N + f - hh * dp.N : row * ald + f) * 2u;
+    }
+  } else if (!prob1) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = 2 * (u * 8 + wave) + (lane >> 5);
+      const int col = min(8 * ((lane & 31) ^ dw_swz(row)), I - i0 - 8);
+      da_cursor_init(cur[u], dp, HN, i0 + col, mbeg + row, M);
+    }
+  }
+
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int s) {
     const int st = s % STAGES;
     const uint32_t lds = lds0 + (uint32_t)(st * 2 * kDwSlab) * 2u;
     const int m0 = mbeg + s * kDwBK;
-    dw_issue(lds, wave, asrc, lda, m0, M, i0, I);
+    if (FAST) {
+      const bf16_bits* base = asrc + (size_t)arow * ald;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) g2lds16_s(base, avoff[u], lds + (uint32_t)(u * 8 + wave) * 1024u);
+      arow += kDwBK;
+      stt += kDwBK;
+      if (stt == dp.T) {
+        stt = 0;
+        arow += bstep;
+      }
+    } else if (prob1) {
+      dw_issue(lds, wave, p.dy, C, m0, M, i0, I);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) g2lds16(da_cursor_next(cur[u], dp.T, M), lds + (uint32_t)(u * 8 + wave) * 1024u);
+    }
     dw_issue(lds + kDwSlab * 2, wave, bsrc, ldb, m0, M, j0, J);
   };
 
@@ -492,7 +637,10 @@ int dw_splits(int M, int C, int HN) {
 
 hipError_t launch_dw_partial(const DwParams& p, hipStream_t s) {
   const int tiles = (4 * p.HN / kDwTile) * (p.C / kDwTile) + (p.C / kDwTile) * ((p.HN + kDwTile - 1) / kDwTile);
-  hipLaunchKernelGGL(dw_partial_kernel, dim3(tiles * p.splits), dim3(512), 0, s, p);
+  if (p.da.T % kDwBK == 0 && p.HN % kDwTile == 0)
+    hipLaunchKernelGGL(dw_partial_kernel<true>, dim3(tiles * p.splits), dim3(512), 0, s, p);
+  else
+    hipLaunchKernelGGL(dw_partial_kernel<false>, dim3(tiles * p.splits), dim3(512), 0, s, p);
   return hipGetLastError();
 }
 

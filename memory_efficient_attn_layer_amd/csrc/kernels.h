@@ -61,10 +61,12 @@ struct AttnBwdParams {
   const float *f1, *f2;                     // (T_max, N)
   const float* rx;                          // (M)
   const float *rq, *rk;                     // (B, H, T)
-  bf16_bits *daq, *dak, *dav;               // (M, H*N) column blocks of the (M, 4*H*N)
-                                            // gradient, row stride ld_da; rows scaled by rx
+  // Gradients of the q, k, v projection outputs, (B, H, T, N), rows scaled
+  // by rx. dak / dav may be k / v themselves: the dK/dV kernel reads only
+  // its own key rows of k and v, each before writing them.
+  bf16_bits *daq, *dak, *dav;
   float *df1, *df2;                         // (T, N) accumulators or null
-  int B, H, T, ld_da;
+  int B, H, T;
   float scale;                              // softmax scale 1/sqrt(N)
   float sl2e;                               // must be 1: stored q . k is in log2 units
   float qscale;                             // stored q = q * qscale
@@ -96,16 +98,25 @@ struct DzParams {
   bf16_bits* sig;                           // (M, HN): sigmoid(a_g) in, z out
   const float* rx;                          // (M)
   bf16_bits* dO;                            // (B, H, T, N)
-  bf16_bits* dag;                           // (M, HN) block of the (M, 4HN) gradient
+  bf16_bits* dag;                           // (M, HN), row stride ld_dag
   float* delta;                             // (B, H, T)
-  int M, T, C, H, N, ld_da;
+  int M, T, C, H, N, ld_dag;
 };
 hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s);
 
-// acc = [daq|dak|dav|dag] Wcat  (rows pre-scaled by rx), then the input
-// RMSNorm backward: dx = acc - x * rx^2 * (acc . x) / C.
+// The gradient of the four projection outputs, da = [da_q | da_k | da_v |
+// da_g] (M, 4*HN), rows pre-scaled by rx, as the dx and dW GEMMs read it:
+// da_q, da_k, da_v head-major (B, H, T, N) like q, k, v; da_g token-major
+// (M, HN) with row stride ld_g.
+struct DaParts {
+  const bf16_bits *q, *k, *v, *g;
+  int ld_g, B, T, H, N;
+};
+
+// acc = da Wcat, then the input RMSNorm backward:
+// dx = acc - x * rx^2 * (acc . x) / C.
 struct DxParams {
-  const bf16_bits* da;                      // (M, 4*HN) = [da_q | da_k | da_v | da_g]
+  DaParts da;
   const bf16_bits* wcatT;                   // (C, 4*HN)
   const bf16_bits* x;                       // (M, C)
   const float* rx;                          // (M)
@@ -118,7 +129,7 @@ hipError_t launch_dx(const DxParams& p, hipStream_t s);
 //   dWcat = da^T x        (4*HN, C)   da = [da_q | da_k | da_v | da_g]
 //   dWo   = dy^T z        (C, HN)     z = O * sig
 struct DwParams {
-  const bf16_bits* da;                      // (M, 4*HN)
+  DaParts da;
   const bf16_bits* x;                       // (M, C)
   const bf16_bits* dy;                      // (M, C)
   const bf16_bits* z;                       // (M, HN)

@@ -99,7 +99,8 @@ def test_pointer_and_workspace_validation(lib):
     # Workspace too small.
     assert lib.mea_fwd(ctypes.byref(d), fake, *args[1:], 10, None) == _header_enum("MEA_ERR_WORKSPACE")
     # mea_bwd pointers: dy x wq wk wv wg wo f1 f2 o lse dx dwq dwk dwv dwg dwo df1 df2 ws
-    bargs = [fake] * 20
+    # (distinct, far apart: dx may overlap nothing else)
+    bargs = [(1 << 32) + i * (1 << 28) for i in range(20)]
     b_dwo_null = list(bargs)
     b_dwo_null[16] = None
     assert lib.mea_bwd(ctypes.byref(d), *b_dwo_null, 10, None) == _header_enum("MEA_ERR_NULL")
@@ -107,6 +108,12 @@ def test_pointer_and_workspace_validation(lib):
     b_one_df[18] = None
     assert lib.mea_bwd(ctypes.byref(d), *b_one_df, 10, None) == _header_enum("MEA_ERR_NULL")
     assert lib.mea_bwd(ctypes.byref(d), *bargs, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
+    # dx overlapping another argument (it holds a transient before the
+    # result): refused before the workspace is even looked at.
+    for other in (0, 1, 9, 19):
+        b_alias = list(bargs)
+        b_alias[11] = bargs[other] + (4096 if other != 19 else 0)  # the workspace is 10 bytes here
+        assert lib.mea_bwd(ctypes.byref(d), *b_alias, 10, None) == _header_enum("MEA_ERR_ALIAS")
     # C > 1024 is forward-only.
     d2 = _d(C=2048)
     assert lib.mea_bwd(ctypes.byref(d2), *bargs, 1 << 40, None) == _header_enum("MEA_ERR_MODEL_DIM")
@@ -163,7 +170,7 @@ def test_varlen_validation(lib):
     assert lib.mea_fwd_varlen(ctypes.byref(d), None, 4, 300, *fargs, 10, None) == _header_enum("MEA_ERR_NULL")
     assert lib.mea_fwd_varlen(ctypes.byref(d), fake + 2, 4, 300, *fargs, 10, None) == _header_enum("MEA_ERR_ALIGN")
     # bwd: dy x wq wk wv wg wo f1 f2 o lse dx dwq dwk dwv dwg dwo df1 df2 ws
-    bargs = [fake] * 20
+    bargs = [(1 << 32) + i * (1 << 28) for i in range(20)]
     assert lib.mea_bwd_varlen(ctypes.byref(d), fake, 4, 300, *bargs, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
     assert lib.mea_bwd_varlen(ctypes.byref(_d(B=1, T=1000, T_max=300, C=2048)), fake, 4, 300, *bargs, 1 << 40,
                               None) == _header_enum("MEA_ERR_MODEL_DIM")
