@@ -232,7 +232,7 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
   const int wf = wave % WF, wt = wave / WF;
   const bf16_bits* wt_g = p.wcatT;  // (C, 4HN)
   const DaParts& dp = p.da;
-  const int HN = p.HN, N = dp.N, T = dp.T;
+  const int N = dp.N, T = dp.T;
 
   // Token rows of the da slabs: group u of load instructions starts at token
   // mf(u); hm(m) is token m's row in a head-major array, in units of N from
