@@ -383,7 +383,8 @@ hipError_t launch_dx(const DxParams& p, hipStream_t s) {
 // Weight gradients D(i, j) = sum_m A(m, i) B(m, j) over a token range:
 //   problem 0: A = da (M, 4HN), B = x (M, C)   -> dWcat (4HN, C)
 //   problem 1: A = dy (M, C),   B = z (M, HN)  -> dWo   (C, HN)
-// Both operands are token-major. Slabs of 32 tokens x 256 features land in
+// Operands run along tokens (da's head-major parts are read per head as
+// (B, T) rows of N, see DaParts). Slabs of 32 tokens x 256 features land in
 // LDS row-major (direct global->LDS loads, 3 stages); the MFMA operands,
 // which run along tokens, are read with the transposing ds_read_b64_tr_b16.
 // Tile 256 x 256, eight waves of 64 (i) x 128 (j). The token range is split

@@ -87,7 +87,7 @@ hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s);
 
 // dZ = dy Wo, then the gate backward:
 //   dO = dZ * sig            -> (B, H, T, N)
-//   da_g = rx * dZ * O * sig * (1 - sig)   -> (M, HN), row stride ld_da
+//   da_g = rx * dZ * O * sig * (1 - sig)   -> (M, HN), row stride ld_dag
 //   delta = rowsum_N(dO * O) -> (B, H, T)
 //   z = O * sig              -> (M, HN), written over sig (the output
 //                               projection's input, for dWo)
