@@ -156,6 +156,10 @@ __device__ __forceinline__ bf16x8 frag_from2(const u32x2& a, const u32x2& b) {
 // 16-byte global load / store.
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+// Non-temporal (streaming) 16-byte store: for outputs not read again soon.
+__device__ __forceinline__ void st16_nt(void* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
 
 // Cross-lane helpers. xor 1 / xor 2 use DPP quad permutes; wider distances go
 // through ds_bpermute (no memory traffic).

@@ -103,9 +103,16 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   constexpr int NUW = SlabPlan<BF, 4, BK>::NU, NUX = SlabPlan<BT, 4, BK>::NU;
   const bf16_bits* wbase[NUW];
   const bf16_bits* xbase[NUX];
-  int iss_ti = 0, iss_ks = 0, iss_st = 0;
+  // iss_rot: the tile's head staggers its k order (slab kk = (ks + h) mod nk
+  // is issued at step ks), so the 8 head tiles of a token tile that run
+  // together on an XCD request each x slab at different times: the first
+  // request fetches it into L2, the others hit (requested together, most
+  // of them went past L2). The outputs are stored non-temporally so that
+  // they do not evict the x slabs and weights from L2.
+  int iss_ti = 0, iss_ks = 0, iss_st = 0, iss_rot = 0;
   auto plan_tile = [&](int ti) {
     const ProjTile tl = proj_tile<N>(start + j0 + ti * nj, H);
+    iss_rot = tl.h % nk;
     const bf16_bits* wseg[NSEG];
     if (NSEG == 4) {
       // [q; v; k; g]: each wave's 128 features hold one rotary projection.
@@ -130,7 +137,8 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   };
   auto issue_next = [&]() {
     const uint32_t lds = lds0 + (uint32_t)(iss_st * STAGE) * 2u;
-    const int k0 = iss_ks * BK;
+    const int kk = iss_ks + iss_rot >= nk ? iss_ks + iss_rot - nk : iss_ks + iss_rot;
+    const int k0 = kk * BK;
     slab_issue_planned<BF, 4, BK>(lds, wave, wplan, [&](int u) { return wbase[u] + k0; });
     slab_issue_planned<BT, 4, BK>(lds + BF * BK * 2, wave, xplan, [&](int u) { return xbase[u] + k0; });
     iss_st = iss_st == NS - 1 ? 0 : iss_st + 1;
@@ -283,10 +291,10 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
         const int tl_row = wt * (TB * 16) + tb * 16 + row;
         const u32x4 val = *reinterpret_cast<const u32x4*>(stg + (gi * 16 + row) * SP + ch * 8);
         if (whole) {
-          st16(tile0 + (uint32_t)(tl_row * (int)tstride + ch * 8), val);
+          st16_nt(tile0 + (uint32_t)(tl_row * (int)tstride + ch * 8), val);
         } else if (m0 + tl_row < M) {
           const int m = m0 + tl_row, bb = m / T, tt = m - bb * T;
-          st16(dstp + (size_t)bb * bstride + (size_t)tt * tstride + ch * 8, val);
+          st16_nt(dstp + (size_t)bb * bstride + (size_t)tt * tstride + ch * 8, val);
         }
       }
     };
