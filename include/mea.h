@@ -29,7 +29,9 @@
  *     Pointers must be 16-byte aligned.
  *
  * Supported shapes: N in {64, 128}; C a multiple of 256 with C <= 1024 for
- * the backward pass (C <= 4096 forward); H >= 1; B, T >= 1; T <= T_max.
+ * the backward pass (C <= 4096 forward); H >= 1; B, T >= 1; T <= T_max; and
+ * for the backward H * (T + 256) * N < 2^30 (one batch's head-major gradient
+ * rows are addressed with 32-bit byte offsets).
  */
 #ifndef MEA_H
 #define MEA_H

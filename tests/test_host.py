@@ -66,6 +66,13 @@ def test_workspace_bytes(lib):
     # Invalid descriptors report 0.
     for bad in (_d(N=96), _d(C=300), _d(T_max=10), _d(eps=0.0), _d(B=0)):
         assert lib.mea_workspace_bytes(ctypes.byref(bad), 0) == 0
+    # The backward's head-major gradient offsets limit H * (T + 256) * N to
+    # 2^30; the forward has no such limit.
+    long_t = _d(B=1, T=1 << 20, T_max=1 << 20, C=1024, H=8, N=128)
+    assert lib.mea_workspace_bytes(ctypes.byref(long_t), _lib.MEA_PASS_FWD) > 0
+    assert lib.mea_workspace_bytes(ctypes.byref(long_t), _lib.MEA_PASS_BWD) == 0
+    ok_t = _d(B=1, T=(1 << 20) - 512, T_max=1 << 20, C=1024, H=8, N=128)
+    assert lib.mea_workspace_bytes(ctypes.byref(ok_t), _lib.MEA_PASS_BWD) > 0
 
 
 @pytest.mark.parametrize(
