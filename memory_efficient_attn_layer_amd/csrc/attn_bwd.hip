@@ -137,9 +137,9 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // ---------------------------------------------------------------------------
 // dQ
 //
-// One workgroup = one (batch, head) and BQ = 4*QW queries; wave w owns QW
-// consecutive queries (64 for N = 64, 32 for N = 128) whose q and dO rows
-// stay in registers as the B operands of
+// One workgroup = one (batch, head) and BQ = 4*QW queries; wave w owns QW =
+// 32 consecutive queries whose q and dO rows stay in registers as the B
+// operands of
 //   S^T = K Q^T   and   dP^T = V dO^T      (A = K, V rows from LDS)
 // on v_mfma_f32_32x32x16_bf16. The query index sits on the lane, so the row
 // statistics ride along as one more k-block of those products (stored q is
@@ -152,10 +152,12 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // ds_read_b64_tr_b16. Key tiles of 64 stream through LDS (global_load_lds,
 // double-buffered, one barrier per tile); tiles wholly below a wave's first
 // query run in a branch-free loop, the rest of the diagonal region after it.
+// For N = 64 three workgroups share a CU (164 registers): 64 queries per wave
+// (two blocks sharing every K/V fragment) held two per SIMD ran 4.4% slower.
 // ---------------------------------------------------------------------------
 template <int N, bool VARLEN>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
-  constexpr int QW = N == 64 ? 64 : 32;  // queries per wave
+__global__ __launch_bounds__(256, N == 64 ? 3 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
+  constexpr int QW = 32;                 // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
   constexpr int BQ = 4 * QW;             // queries per workgroup
   constexpr int BKV = 64;                // keys per LDS tile
@@ -651,7 +653,7 @@ __global__ __launch_bounds__(256, N == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(Att
 
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
   if (p.sl2e != 1.0f) return hipErrorInvalidValue;  // stored q must be in log2 units
-  const int BQ = N == 64 ? 256 : 128;
+  const int BQ = 128;
   const bool var = p.cu != nullptr;
   const int G = var ? p.nseq * p.H * ((p.max_len + BQ - 1) / BQ) : p.B * p.H * ((p.T + BQ - 1) / BQ);
   if (N == 64 && !var)

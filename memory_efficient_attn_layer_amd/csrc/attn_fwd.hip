@@ -5,8 +5,10 @@
 // scale = 1/sqrt(N) (:426), causal, no dropout, returning the output and the
 // natural-log row normaliser (lse).
 //
-// One workgroup = one (batch, head) and BQ = 4*QW queries; wave w owns QW
-// consecutive queries (QW = 64 for N = 64, 32 for N = 128). Keys stream
+// One workgroup = one (batch, head) and BQ = 4*QW queries; wave w owns QW =
+// 32 consecutive queries (for N = 64, 110 registers: four workgroups per
+// CU; 64 queries per wave, two per SIMD with a software-pipelined tile,
+// ran 10% slower). Keys stream
 // through LDS in tiles of 64, loaded straight from global memory into a
 // swizzled row-major layout (global_load_lds, double-buffered, one barrier
 // per tile). Each tile is consumed in two 32-key steps with
@@ -44,8 +46,8 @@ namespace mea {
 // (sequence, h, query block) and every row index is taken relative to the
 // sequence's first token.
 template <int N, bool VARLEN>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
-  constexpr int QW = N == 64 ? 64 : 32;  // queries per wave
+__global__ __launch_bounds__(256, N == 64 ? 4 : 2) void attn_fwd_kernel(AttnFwdParams p) {
+  constexpr int QW = 32;  // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
   constexpr int BQ = 4 * QW;             // queries per workgroup
   constexpr int BKV = 64;                // keys per LDS tile
@@ -263,85 +265,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     }
   };
 
-  // A whole unmasked 64-key tile in the fixed-offset form (two query blocks
-  // per wave), written as a software pipeline over its four 32x32 blocks
-  // (step st, query block qb): the exp2 / convert work of one block is
-  // issued between the MFMAs of the next block's S^T and of the previous
-  // block's O^T update, so one wave keeps the matrix core fed while its own
-  // VALU work runs. Phases are fenced with sched_barrier and interleaved with
-  // sched_group_barrier patterns (MFMA, VALU, DS read).
-  auto tile_fixed = [&](const bf16_bits* ks_t, const bf16_bits* vs_t, auto fixed_tag) {
-    static_assert(decltype(fixed_tag)::value && QB == 2, "fixed offset, two query blocks per wave");
-    bf16x8 kf[2][KS], vf[2][2][DB], pf[2][2][2];
-    f32x16 s[2][2];
-    auto load_k = [&](int st) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        kf[st][ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + st * 32 * N + koff[ks]));
-    };
-    auto load_v = [&](int st) {
-#pragma unroll
-      for (int kst = 0; kst < 2; ++kst)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const bf16_bits* vr = vs_t + (st * 32 + 16 * kst) * N;
-          vf[st][kst][db] = frag_from2(lds_read_tr4(vr + voff[0][db]), lds_read_tr4(vr + voff[1][db]));
-        }
-    };
-    auto S = [&](int st, int qb) {
-      s[st][qb] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s[st][qb] = mfma32(kf[st][ks], qf[qb][ks], s[st][qb]);
-    };
-    auto E = [&](int st, int qb) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[st][qb][i] = fast_exp2(s[st][qb][i]);
-#pragma unroll
-      for (int kst = 0; kst < 2; ++kst) {
-        u32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = pack2(s[st][qb][8 * kst + 2 * e], s[st][qb][8 * kst + 2 * e + 1]);
-        pf[st][qb][kst] = as_frag(w);
-      }
-    };
-    auto PV = [&](int st, int qb) {
-#pragma unroll
-      for (int kst = 0; kst < 2; ++kst) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[qb][db] = mfma32(vf[st][kst][db], pf[st][qb][kst], o[qb][db]);
-        lsum[qb] = mfma(sel, pf[st][qb][kst], lsum[qb]);
-      }
-    };
-    constexpr int PVM = 2 * DB + 2;  // MFMAs of one PV()
-    load_k(0);
-    S(0, 0);
-    load_v(0);
-    load_k(1);
-    __builtin_amdgcn_sched_barrier(0);
-    S(0, 1);
-    E(0, 0);
-    sched_pattern<KS, 1, 24 / KS, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    PV(0, 0);
-    S(1, 0);
-    E(0, 1);
-    load_v(1);
-    sched_pattern<8, 1, 3, 1>();
-    sched_pattern<1, PVM + KS - 8, 0, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    PV(0, 1);
-    S(1, 1);
-    E(1, 0);
-    sched_pattern<8, 1, 3, 0>();
-    sched_pattern<1, PVM + KS - 8, 0, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    PV(1, 0);
-    E(1, 1);
-    sched_pattern<PVM, 1, 24 / PVM, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    PV(1, 1);
-  };
-
   // Tiles wholly below a wave's first query (and inside the sequence) need
   // no mask for that wave and run in a branch-free loop; the rest of the
   // diagonal region and a ragged sequence end follow in a second loop. The
@@ -358,12 +281,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
       if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
       const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
       const bf16_bits* vs_t = ks_t + TILE;
-      if constexpr (decltype(fixed_tag)::value && QB == 2) {
-        tile_fixed(ks_t, vs_t, fixed_tag);
-      } else {
-        step(ks_t, vs_t, 0, j * BKV, fixed_tag, std::false_type{});
-        step(ks_t, vs_t, 1, j * BKV + 32, fixed_tag, std::false_type{});
-      }
+      step(ks_t, vs_t, 0, j * BKV, fixed_tag, std::false_type{});
+      step(ks_t, vs_t, 1, j * BKV + 32, fixed_tag, std::false_type{});
       wait_vmcnt0();
       __syncthreads();
     }
@@ -424,7 +343,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
 }
 
 hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s) {
-  const int BQ = N == 64 ? 256 : 128;
+  const int BQ = 128;
   const bool var = p.cu != nullptr;
   const int G = var ? p.nseq * p.H * ((p.max_len + BQ - 1) / BQ) : p.B * p.H * ((p.T + BQ - 1) / BQ);
   if (N == 64 && !var)

@@ -94,20 +94,6 @@ __device__ __forceinline__ void g2lds16_s(const void* sbase, uint32_t voff, uint
 // LDS byte address of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)((lds_void*)p); }
 
-// Scheduling hint for the current scheduling region (fenced by
-// __builtin_amdgcn_sched_barrier): REP repetitions of NM MFMAs, then NV other
-// VALU instructions, then ND LDS reads, filled in that order by the
-// compiler's instruction-group scheduler; empty groups are left out.
-template <int REP, int NM, int NV, int ND>
-__device__ __forceinline__ void sched_pattern() {
-#pragma unroll
-  for (int r = 0; r < REP; ++r) {
-    if (NM) __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
-    if (NV) __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
-    if (ND) __builtin_amdgcn_sched_group_barrier(0x100, ND, 0);
-  }
-}
-
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left open), as a builtin so the
 // compiler's own wait tracking also sees every earlier vector load retired.
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
