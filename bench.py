@@ -12,7 +12,7 @@ the dominant kernel (timed live with HIP events on its launch stream over the
 timed region), peak HBM, and the CPU baseline (the fp32 oracle on a bounded
 batch slice on the host cores). Progress goes to stderr.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--compare-eager] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-eager] [--no-cpu-baseline] [--table-grad]
     python bench.py --workload 2|3       # the same line for another fwd+bwd workload
     python bench.py --workload 4         # forward-only (prefill) workload: fwd tokens/s, no CPU leg
     python bench.py --workload W --varlen  # B packed sequences of seeded lengths in [T/4, T], fwd+bwd
@@ -67,6 +67,17 @@ def kernel_work(w):
     }
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (first processor entry of /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w, seconds: float):
     """The fp32 oracle (eager block, CPU) on a batch slice of the workload."""
     import torch
@@ -92,6 +103,7 @@ def cpu_baseline(w, seconds: float):
         "value": w.T / med,
         "unit": "tokens/s",
         "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"fp32 oracle fwd+bwd (oracle/block.py) on 1 of {w.B} sequences (T={w.T}, C={w.C}, "
                   f"H={w.H}, N={w.N}); 1 warm-up + {len(times)} timed iterations, median {med:.2f} s",
@@ -157,7 +169,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", type=int, default=1, help="workload id (1 = the north-star shape)")
-    ap.add_argument("--compare-eager", action="store_true", help="also time the eager SDPA path on the GPU")
+    ap.add_argument("--no-eager", action="store_true",
+                    help="skip the eager checkpoint+SDPA comparator (timed and peak HBM on the same GPU)")
+    ap.add_argument("--table-grad", action="store_true",
+                    help="also differentiate the rotary tables (dF1 / dF2, as the reference always does)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--varlen", action="store_true",
@@ -207,12 +222,18 @@ def main():
     x = inp["x"].requires_grad_(True)
     ws = [inp[n].requires_grad_(True) for n in ("wq", "wk", "wv", "wg", "wo")]
     f1, f2, dy = inp["f1"], inp["f2"], inp["dy"]
+    wrt = [x, *ws]
+    if args.table_grad:
+        # Trainable tables, differentiated like every other input.
+        f1 = f1.float().requires_grad_(True)
+        f2 = f2.float().requires_grad_(True)
+        wrt += [f1, f2]
     H, N = w.H, w.N
     sync = torch.cuda.synchronize
 
     def step():
         y = FusedAttentionFunction.apply(x, *ws, f1, f2, H, N, 1e-6)
-        return torch.autograd.grad(y, [x, *ws], dy)
+        return torch.autograd.grad(y, wrt, dy)
 
     log("warm-up")
     for _ in range(max(1, args.warmup)):
@@ -268,12 +289,12 @@ def main():
         attention = None
 
     eager = None
-    if args.compare_eager:
+    if not args.no_eager:
         log("eager SDPA comparator")
         try:
             def estep():
                 y = eager_block(x, *ws, f1, f2, H, N)
-                return torch.autograd.grad(y, [x, *ws], dy)
+                return torch.autograd.grad(y, wrt, dy)
 
             epeak = peak_of(estep, sync)
             esec = measure(estep, max(3, args.steps // 4), 2, sync)
@@ -303,8 +324,10 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": w.name, "B": w.B, "T": w.T, "C": w.C, "H": H, "N": N,
-                   "tokens_per_step": tokens, "parallelism": "single-gpu"},
-        "peak_hbm": {"fused_bytes": int(peak), "eager_sdpa": eager},
+                   "tokens_per_step": tokens, "table_grad": bool(args.table_grad), "parallelism": "single-gpu"},
+        "peak_hbm": {"fused_bytes": int(peak), "eager_sdpa": eager,
+                     "fused_below_eager": None if not eager or "peak_hbm_bytes" not in eager
+                     else bool(peak < eager["peak_hbm_bytes"])},
         "block_tflops": round(3 * w.flops_fwd() / sec / 1e12, 2),
         "roofline": roofline,
         "attention": attention,

@@ -240,6 +240,31 @@ int mea_attn_fwd(const mea_desc* d, const void* q, const void* k,
 int mea_gate_oproj(const mea_desc* d, const void* o, const void* sig,
                    const void* wo, void* y, void* stream);
 
+/*
+ * Stage: the first half of mea_bwd, stopping before the weight and input
+ * gradients. Runs the recompute (fast_triton_attn.py:500-570), the o_proj
+ * and gate backward (:577-584, :601), the aten flash backward (:586-596)
+ * and the exact q/k RMSNorm + rotary backward (in place of :603-620), and
+ * returns what the reference holds at :641 as the inputs of its dW / dx
+ * GEMMs, plus the attention-backward operands:
+ *
+ *   daq, dak, dav   (B, H, T, N) bf16   rx * dL/da_q, rx * dL/da_k, rx * dL/da_v
+ *   dag             (B, T, H*N) bf16    rx * dL/da_g
+ *   dO              (B, H, T, N) bf16   dL/dO (the attention output's gradient)
+ *   delta           (B, H, T) fp32      rowsum(dO * O)
+ *   df1, df2        as in mea_bwd (may be NULL together)
+ *
+ * rx = 1/rms(x) per token; a_p = rmsnorm(x) W_p^T. All other arguments and
+ * the workspace as in mea_bwd. Used to check the backward per row.
+ */
+int mea_bwd_stage_grads(const mea_desc* d, const void* dy, const void* x,
+                        const void* wq, const void* wk, const void* wv,
+                        const void* wg, const void* wo, const float* f1,
+                        const float* f2, const void* o_save,
+                        const float* lse_save, void* daq, void* dak, void* dav,
+                        void* dag, void* dO, float* delta, float* df1,
+                        float* df2, void* ws, size_t ws_bytes, void* stream);
+
 /* Text for a status code returned by any entry point. */
 const char* mea_strerror(int code);
 

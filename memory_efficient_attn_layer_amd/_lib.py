@@ -61,6 +61,10 @@ EXPORTS = {
     "mea_qkvg_proj": (ctypes.c_int, [_desc] + [_vp] * 5 + [_fp, _fp] + [_vp] * 4 + [_fp, _fp, _fp, _vp]),
     "mea_attn_fwd": (ctypes.c_int, [_desc, _vp, _vp, _vp, _vp, _fp, _vp]),
     "mea_gate_oproj": (ctypes.c_int, [_desc, _vp, _vp, _vp, _vp, _vp]),
+    "mea_bwd_stage_grads": (
+        ctypes.c_int,
+        [_desc] + [_vp] * 7 + [_fp, _fp, _vp, _fp] + [_vp] * 5 + [_fp, _fp, _fp, _vp, ctypes.c_size_t, _vp],
+    ),
     "mea_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "mea_version": (ctypes.c_char_p, []),
     "mea_profile_enable": (ctypes.c_int, [ctypes.c_int]),

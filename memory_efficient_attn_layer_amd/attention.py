@@ -79,14 +79,32 @@ def _tables32(factor1: torch.Tensor, factor2: torch.Tensor, T: int):
     return factor1[:T].float().contiguous(), factor2[:T].float().contiguous()
 
 
+def _wants_grad(*tensors) -> bool:
+    """Whether autograd will record the op: grad mode is on and an input
+    requires grad. Decided by the caller of ``Function.apply``: inside
+    ``forward`` grad mode is always off and ``ctx.needs_input_grad`` ignores
+    it (a Parameter reports True even under ``torch.no_grad()``)."""
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+
+
 class FusedAttentionFunction(torch.autograd.Function):
-    """Autograd op of the block (fast_triton_attn.py:373-675)."""
+    """Autograd op of the block (fast_triton_attn.py:373-675).
+
+    ``apply(x, Wq, Wk, Wv, Wg, Wo, factor1, factor2, H, N, eps)`` as in the
+    reference (:685-697). Without a gradient requirement (grad mode off, or
+    no input requiring grad) the forward saves nothing and writes no O / lse.
+    """
+
+    @classmethod
+    def apply(cls, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H, N, eps=1e-6):
+        save = _wants_grad(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2)
+        return super().apply(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H, N, eps, save)
 
     @staticmethod
-    def forward(ctx, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H, N, eps):
+    def forward(ctx, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H, N, eps, save):
         H, N, eps = int(H), int(N), float(eps)
         weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
-        need_bwd = any(ctx.needs_input_grad[:8])
+        need_bwd = bool(save)
         _validate(x, weights, factor1, factor2, H, N, eps, need_bwd)
         lib = _lib.load()
         B, T, C = x.shape
@@ -149,7 +167,7 @@ class FusedAttentionFunction(torch.autograd.Function):
             gf2 = torch.zeros_like(factor2)
             gf1[:T] = df1.to(factor1.dtype)
             gf2[:T] = df2.to(factor2.dtype)
-        return (dx, *dws, gf1, gf2, None, None, None)
+        return (dx, *dws, gf1, gf2, None, None, None, None)
 
 
 def fused_attn(x, q_proj, k_proj, v_proj, g_proj, o_proj, yarn_module, H, N, eps=1e-6):
@@ -178,14 +196,21 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
     Gradients as in FusedAttentionFunction; table gradients cover rows
     0 .. max_len - 1."""
 
+    @classmethod
+    def apply(cls, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, cu_seqlens, max_len, H, N,
+              eps=1e-6):
+        save = _wants_grad(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2)
+        return super().apply(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, cu_seqlens,
+                             max_len, H, N, eps, save)
+
     @staticmethod
     def forward(ctx, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, cu_seqlens, max_len, H,
-                N, eps):
+                N, eps, save):
         H, N, eps, max_len = int(H), int(N), float(eps), int(max_len)
         weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
         if not isinstance(x, torch.Tensor) or x.dim() != 2:
             raise ValueError("x must be a (total_tokens, C) tensor")
-        need_bwd = any(ctx.needs_input_grad[:8])
+        need_bwd = bool(save)
         # Dtypes, devices, widths and weight shapes (tables: rows checked against max_len below).
         _validate(x[:1].unsqueeze(0), weights, factor1, factor2, H, N, eps, need_bwd)
         total, C = x.shape
@@ -263,7 +288,7 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
             gf2 = torch.zeros_like(factor2)
             gf1[:max_len] = df1.to(factor1.dtype)
             gf2[:max_len] = df2.to(factor2.dtype)
-        return (dx, *dws, gf1, gf2, None, None, None, None, None)
+        return (dx, *dws, gf1, gf2, None, None, None, None, None, None)
 
 
 def fused_attn_varlen(x, q_proj, k_proj, v_proj, g_proj, o_proj, yarn_module, H, N, cu_seqlens, max_len=None,

@@ -349,16 +349,138 @@ int fwd_impl(const mea_desc* d, const Varlen* var, const void* x, const void* wq
   return gate_oproj_launch(d, o, sig, wo, y, stream);
 }
 
+// Buffers of one backward pass inside the workspace (and dx).
+struct BwdBufs {
+  bf16_bits *q, *k, *v, *sig, *dO, *daq, *dag, *woT, *wcatT;
+  float *rx, *rq, *rk, *delta, *part;
+  int ld_dag;
+};
+
+BwdBufs bwd_bufs(const mea_desc* d, void* ws, void* dag_ext, int ld_dag_ext) {
+  const Layout L = make_layout(*d, MEA_PASS_BWD);
+  BwdBufs b;
+  b.q = at<bf16_bits>(ws, L.q);
+  b.k = at<bf16_bits>(ws, L.k);
+  b.v = at<bf16_bits>(ws, L.v);
+  b.sig = at<bf16_bits>(ws, L.sig);
+  b.dO = at<bf16_bits>(ws, L.dO);
+  b.daq = at<bf16_bits>(ws, L.daq);
+  b.dag = dag_ext != nullptr ? static_cast<bf16_bits*>(dag_ext) : at<bf16_bits>(ws, L.dag);
+  b.ld_dag = dag_ext != nullptr ? ld_dag_ext : (int)(d->H * d->N);
+  b.woT = at<bf16_bits>(ws, L.woT);
+  b.wcatT = at<bf16_bits>(ws, L.wcatT);
+  b.rx = at<float>(ws, L.rx);
+  b.rq = at<float>(ws, L.rq);
+  b.rk = at<float>(ws, L.rk);
+  b.delta = at<float>(ws, L.delta);
+  b.part = at<float>(ws, L.part);
+  return b;
+}
+
+// First half of the backward: weight transposes, the recompute of q, k, v,
+// sigmoid(g) and the RMS statistics, dZ with the gate backward, and the
+// attention backward with the exact q/k chain. Leaves the projection-output
+// gradients (rows scaled by rx) in bf.daq, bf.k (da_k), bf.v (da_v) and
+// bf.dag, and dO / delta in their buffers.
+int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* x, const void* wq, const void* wk,
+              const void* wv, const void* wg, const void* wo, const float* f1, const float* f2, const void* o_save,
+              const float* lse_save, float* df1, float* df2, const BwdBufs& bf, void* ws, void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = (int)(d->B * d->T), T = (int)d->T, H = (int)d->H, N = (int)d->N, C = (int)d->C;
+  const int HN = H * N;
+  const Layout L = make_layout(*d, MEA_PASS_BWD);
+
+  // Weight transposes (k-contiguous B operands for dZ and dx).
+  MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_transpose(static_cast<const bf16_bits*>(wo), C, HN, HN, bf.woT, C, 0, s); }));
+  const void* wp[4] = {wq, wk, wv, wg};
+  for (int j = 0; j < 4; ++j)
+    MEA_TRY(timed(K_TRANSPOSE, s, [&] {
+      return mea::launch_transpose(static_cast<const bf16_bits*>(wp[j]), HN, C, C, bf.wcatT, 4 * HN, j * HN, s);
+    }));
+  if (df1 != nullptr) {
+    // Table rows the block touches: positions 0 .. T-1 (packed: max_len - 1).
+    const size_t rows = (size_t)(var != nullptr ? var->max_len : T);
+    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df1, rows * N, s); }));
+    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df2, rows * N, s); }));
+  }
+
+  // Recompute q, k, v, sigmoid(g) and the three RMS statistics.
+  const float qs = q_log2_scale(N);
+  int* tpos = nullptr;
+  if (var != nullptr) {
+    tpos = at<int>(ws, L.tpos);
+    MEA_TRY(mea::launch_token_positions(var->cu, var->nseq, T, tpos, s));
+  }
+  int rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, bf.q, bf.k, bf.v, bf.sig, bf.rx, bf.rq, bf.rk, qs, nullptr, tpos,
+                       stream);
+  if (rc != MEA_OK) return rc;
+
+  mea::DzParams dz;
+  dz.dy = static_cast<const bf16_bits*>(dy);
+  dz.woT = bf.woT;
+  dz.o = static_cast<const bf16_bits*>(o_save);
+  dz.sig = bf.sig;
+  dz.rx = bf.rx;
+  dz.dO = bf.dO;
+  dz.dag = bf.dag;
+  dz.delta = bf.delta;
+  dz.M = M;
+  dz.T = T;
+  dz.C = C;
+  dz.H = H;
+  dz.N = N;
+  dz.ld_dag = bf.ld_dag;
+  MEA_TRY(timed(K_DZ_GATE_BWD, s, [&] { return mea::launch_dz_gate_bwd(dz, s); }));
+
+  mea::AttnBwdParams ab;
+  ab.q = bf.q;
+  ab.k = bf.k;
+  ab.v = bf.v;
+  ab.dO = bf.dO;
+  ab.lse = lse_save;
+  ab.delta = bf.delta;
+  ab.f1 = f1;
+  ab.f2 = f2;
+  ab.rx = bf.rx;
+  ab.rq = bf.rq;
+  ab.rk = bf.rk;
+  ab.daq = bf.daq;
+  ab.dak = bf.k;
+  ab.dav = bf.v;
+  ab.df1 = df1;
+  ab.df2 = df2;
+  ab.B = (int)d->B;
+  ab.H = H;
+  ab.T = T;
+  ab.scale = (float)(1.0 / sqrt((double)N));
+  ab.sl2e = 1.0f;  // q was stored in log2 units by the recompute above
+  ab.qscale = qs;
+  ab.cu = var != nullptr ? var->cu : nullptr;
+  ab.nseq = var != nullptr ? var->nseq : 0;
+  ab.max_len = var != nullptr ? var->max_len : 0;
+  MEA_TRY(timed(K_ATTN_BWD_DQ, s, [&] { return mea::launch_attn_bwd_dq(ab, N, s); }));
+  MEA_TRY(timed(K_ATTN_BWD_DKDV, s, [&] { return mea::launch_attn_bwd_dkdv(ab, N, s); }));
+  return MEA_OK;
+}
+
+// Pointer checks shared by the backward entry points.
+int bwd_check(const mea_desc* d, const Varlen* var, std::initializer_list<const void*> ps, float* df1, float* df2) {
+  int rc = validate_pass(d, MEA_PASS_BWD, var);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs(ps);
+  if (rc != MEA_OK) return rc;
+  if ((df1 == nullptr) != (df2 == nullptr)) return MEA_ERR_NULL;
+  if (df1 != nullptr && (!aligned16(df1) || !aligned16(df2))) return MEA_ERR_ALIGN;
+  return MEA_OK;
+}
+
 int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x, const void* wq, const void* wk,
              const void* wv, const void* wg, const void* wo, const float* f1, const float* f2, const void* o_save,
              const float* lse_save, void* dx, void* dwq, void* dwk, void* dwv, void* dwg, void* dwo, float* df1,
              float* df2, void* ws, size_t ws_bytes, void* stream) {
-  int rc = validate_pass(d, MEA_PASS_BWD, var);
+  int rc = bwd_check(d, var, {dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, dx, dwq, dwk, dwv, dwg, dwo, ws},
+                     df1, df2);
   if (rc != MEA_OK) return rc;
-  rc = check_ptrs({dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, dx, dwq, dwk, dwv, dwg, dwo, ws});
-  if (rc != MEA_OK) return rc;
-  if ((df1 == nullptr) != (df2 == nullptr)) return MEA_ERR_NULL;
-  if (df1 != nullptr && (!aligned16(df1) || !aligned16(df2))) return MEA_ERR_ALIGN;
   {
     // dx is written before the end (it holds da_g while HN <= C): it may
     // overlap nothing else.
@@ -378,112 +500,30 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
   const int M = (int)(d->B * d->T), T = (int)d->T, H = (int)d->H, N = (int)d->N, C = (int)d->C;
   const int HN = H * N;
 
-  bf16_bits* q = at<bf16_bits>(ws, L.q);
-  bf16_bits* k = at<bf16_bits>(ws, L.k);
-  bf16_bits* v = at<bf16_bits>(ws, L.v);
-  bf16_bits* sig = at<bf16_bits>(ws, L.sig);
-  bf16_bits* dO = at<bf16_bits>(ws, L.dO);
   // Gradients of the projection outputs: da_q, and da_k / da_v written over
   // k / v by the dK/dV kernel (the last reader of k and v), head-major;
   // da_g token-major, in the rows of dx when they are wide enough (each dx
   // workgroup reads the da_g rows it later overwrites, and nothing else
   // reads them after the weight gradients).
-  bf16_bits* daq = at<bf16_bits>(ws, L.daq);
   const bool dag_in_dx = HN <= C;
-  bf16_bits* dag = dag_in_dx ? static_cast<bf16_bits*>(dx) : at<bf16_bits>(ws, L.dag);
-  const int ld_dag = dag_in_dx ? C : HN;
-  const mea::DaParts da = {daq, k, v, dag, ld_dag, (int)d->B, T, H, N};
-  float* rx = at<float>(ws, L.rx);
-  float* rq = at<float>(ws, L.rq);
-  float* rk = at<float>(ws, L.rk);
-  float* delta = at<float>(ws, L.delta);
-  bf16_bits* woT = at<bf16_bits>(ws, L.woT);
-  bf16_bits* wcatT = at<bf16_bits>(ws, L.wcatT);
-  float* part = at<float>(ws, L.part);
-
-  // Weight transposes (k-contiguous B operands for dZ and dx).
-  MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_transpose(static_cast<const bf16_bits*>(wo), C, HN, HN, woT, C, 0, s); }));
-  const void* wp[4] = {wq, wk, wv, wg};
-  for (int j = 0; j < 4; ++j)
-    MEA_TRY(timed(K_TRANSPOSE, s, [&] {
-      return mea::launch_transpose(static_cast<const bf16_bits*>(wp[j]), HN, C, C, wcatT, 4 * HN, j * HN, s);
-    }));
-  if (df1 != nullptr) {
-    // Table rows the block touches: positions 0 .. T-1 (packed: max_len - 1).
-    const size_t rows = (size_t)(var != nullptr ? var->max_len : T);
-    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df1, rows * N, s); }));
-    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df2, rows * N, s); }));
-  }
-
-  // Recompute q, k, v, sigmoid(g) and the three RMS statistics.
-  const float qs = q_log2_scale(N);
-  int* tpos = nullptr;
-  if (var != nullptr) {
-    tpos = at<int>(ws, L.tpos);
-    MEA_TRY(mea::launch_token_positions(var->cu, var->nseq, T, tpos, s));
-  }
-  rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, qs, nullptr, tpos, stream);
+  const BwdBufs bf = bwd_bufs(d, ws, dag_in_dx ? dx : nullptr, C);
+  rc = bwd_front(d, var, dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, df1, df2, bf, ws, stream);
   if (rc != MEA_OK) return rc;
-
-  mea::DzParams dz;
-  dz.dy = static_cast<const bf16_bits*>(dy);
-  dz.woT = woT;
-  dz.o = static_cast<const bf16_bits*>(o_save);
-  dz.sig = sig;
-  dz.rx = rx;
-  dz.dO = dO;
-  dz.dag = dag;
-  dz.delta = delta;
-  dz.M = M;
-  dz.T = T;
-  dz.C = C;
-  dz.H = H;
-  dz.N = N;
-  dz.ld_dag = ld_dag;
-  MEA_TRY(timed(K_DZ_GATE_BWD, s, [&] { return mea::launch_dz_gate_bwd(dz, s); }));
-
-  mea::AttnBwdParams ab;
-  ab.q = q;
-  ab.k = k;
-  ab.v = v;
-  ab.dO = dO;
-  ab.lse = lse_save;
-  ab.delta = delta;
-  ab.f1 = f1;
-  ab.f2 = f2;
-  ab.rx = rx;
-  ab.rq = rq;
-  ab.rk = rk;
-  ab.daq = daq;
-  ab.dak = k;
-  ab.dav = v;
-  ab.df1 = df1;
-  ab.df2 = df2;
-  ab.B = (int)d->B;
-  ab.H = H;
-  ab.T = T;
-  ab.scale = (float)(1.0 / sqrt((double)N));
-  ab.sl2e = 1.0f;  // q was stored in log2 units by the recompute above
-  ab.qscale = qs;
-  ab.cu = var != nullptr ? var->cu : nullptr;
-  ab.nseq = var != nullptr ? var->nseq : 0;
-  ab.max_len = var != nullptr ? var->max_len : 0;
-  MEA_TRY(timed(K_ATTN_BWD_DQ, s, [&] { return mea::launch_attn_bwd_dq(ab, N, s); }));
-  MEA_TRY(timed(K_ATTN_BWD_DKDV, s, [&] { return mea::launch_attn_bwd_dkdv(ab, N, s); }));
+  const mea::DaParts da = {bf.daq, bf.k, bf.v, bf.dag, bf.ld_dag, (int)d->B, T, H, N};
 
   mea::DwParams dw;
   dw.da = da;
   dw.x = static_cast<const bf16_bits*>(x);
   dw.dy = static_cast<const bf16_bits*>(dy);
-  dw.z = sig;  // the dZ kernel replaced sigmoid(a_g) by z = O * sigmoid(a_g)
-  dw.part = part;
+  dw.z = bf.sig;  // the dZ kernel replaced sigmoid(a_g) by z = O * sigmoid(a_g)
+  dw.part = bf.part;
   dw.M = M;
   dw.C = C;
   dw.HN = HN;
   dw.splits = mea::dw_splits(M, C, HN);
   MEA_TRY(timed(K_DW_PARTIAL, s, [&] { return mea::launch_dw_partial(dw, s); }));
   mea::DwReduceParams dr;
-  dr.part = part;
+  dr.part = bf.part;
   dr.dwq = static_cast<bf16_bits*>(dwq);
   dr.dwk = static_cast<bf16_bits*>(dwk);
   dr.dwv = static_cast<bf16_bits*>(dwv);
@@ -496,9 +536,9 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
 
   mea::DxParams dxp;
   dxp.da = da;
-  dxp.wcatT = wcatT;
+  dxp.wcatT = bf.wcatT;
   dxp.x = static_cast<const bf16_bits*>(x);
-  dxp.rx = rx;
+  dxp.rx = bf.rx;
   dxp.dx = static_cast<bf16_bits*>(dx);
   dxp.M = M;
   dxp.C = C;
@@ -541,6 +581,30 @@ int mea_bwd_varlen(const mea_desc* d, const int32_t* cu_seqlens, int32_t nseq, i
   const Varlen var{cu_seqlens, nseq, max_len};
   return bwd_impl(d, &var, dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, dx, dwq, dwk, dwv, dwg, dwo, df1,
                   df2, ws, ws_bytes, stream);
+}
+
+int mea_bwd_stage_grads(const mea_desc* d, const void* dy, const void* x, const void* wq, const void* wk,
+                        const void* wv, const void* wg, const void* wo, const float* f1, const float* f2,
+                        const void* o_save, const float* lse_save, void* daq, void* dak, void* dav, void* dag,
+                        void* dO, float* delta, float* df1, float* df2, void* ws, size_t ws_bytes, void* stream) {
+  int rc = bwd_check(d, nullptr, {dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, daq, dak, dav, dag, dO, delta, ws},
+                     df1, df2);
+  if (rc != MEA_OK) return rc;
+  const Layout L = make_layout(*d, MEA_PASS_BWD);
+  if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
+  const int HN = (int)(d->H * d->N);
+  // da_g goes straight to the caller's buffer (token-major rows of H*N).
+  const BwdBufs bf = bwd_bufs(d, ws, dag, HN);
+  rc = bwd_front(d, nullptr, dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, df1, df2, bf, ws, stream);
+  if (rc != MEA_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t act = (size_t)(d->B * d->T) * (size_t)HN * 2, stat = (size_t)(d->B * d->H * d->T) * 4;
+  MEA_TRY(hipMemcpyAsync(daq, bf.daq, act, hipMemcpyDeviceToDevice, s));
+  MEA_TRY(hipMemcpyAsync(dak, bf.k, act, hipMemcpyDeviceToDevice, s));
+  MEA_TRY(hipMemcpyAsync(dav, bf.v, act, hipMemcpyDeviceToDevice, s));
+  MEA_TRY(hipMemcpyAsync(dO, bf.dO, act, hipMemcpyDeviceToDevice, s));
+  MEA_TRY(hipMemcpyAsync(delta, bf.delta, stat, hipMemcpyDeviceToDevice, s));
+  return MEA_OK;
 }
 
 int mea_prefill(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,

@@ -130,7 +130,12 @@ class DecodeGraph:
     kernel launches and the Python around them. ``step(x, pos)`` copies x
     (B, C) and pos (B,) into the graph's static inputs, replays, and returns
     the static output (overwritten by the next step; clone it to keep it).
-    Nothing in the captured step clears memory with a memset."""
+    Nothing in the captured step clears memory with a memset.
+
+    Construction does not touch ``cache``: the warm-up steps run on a scratch
+    cache of the same shape (freed afterwards), and capturing records the
+    step without executing it. The cache may therefore be prefilled before
+    or after the graph is built."""
 
     def __init__(self, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H: int, N: int,
                  cache: KVCache, eps: float = 1e-6, warmup: int = 2):
@@ -142,20 +147,22 @@ class DecodeGraph:
         self._cache, self._eps = cache, float(eps)
         self.x = torch.zeros((B, C), device=dev, dtype=torch.bfloat16)
         self.pos = torch.zeros((B,), device=dev, dtype=torch.int32)
-        # Warm-up on a side stream (allocator and library state), writing the
-        # static inputs' zeros into cache row 0 only, then capture.
+        # Warm-up (allocator and library state) on a side stream and a scratch
+        # cache, then capture on the caller's cache.
+        scratch = KVCache(torch.empty_like(cache.k), torch.empty_like(cache.v))
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
             for _ in range(max(1, warmup)):
-                self._run()
+                self._run(scratch)
         torch.cuda.current_stream(dev).wait_stream(side)
+        del scratch
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.y = self._run()
+            self.y = self._run(self._cache)
 
-    def _run(self):
-        return decode_step(self.x, *self._w, self._f1, self._f2, *self._args, self.pos, self._cache, self._eps)
+    def _run(self, cache: KVCache):
+        return decode_step(self.x, *self._w, self._f1, self._f2, *self._args, self.pos, cache, self._eps)
 
     def step(self, x, pos) -> torch.Tensor:
         self.x.copy_(x)

@@ -5,7 +5,13 @@ identical bf16-rounded inputs):
   * bf16 outputs (y and stage outputs): max |gpu - ref| <= 2e-2 * max |ref|
     and relative Frobenius error <= 2e-2;
   * gradients (dx, all five weight gradients, both table gradients):
-    relative Frobenius error ||gpu - ref|| / ||ref|| <= 3e-2.
+    relative Frobenius error ||gpu - ref|| / ||ref|| <= 3e-2;
+  * per row (one token of y and dx; one (b, h, t) row of an attention
+    gradient): ||gpu_r - ref_r|| <= ROW_TOL * max(||ref_r||, ROW_FLOOR *
+    rms_r ||ref_r||). The floor keeps rows whose exact value nearly cancels
+    from demanding more than bf16 operands give; an error confined to a few
+    rows or one key block fails this bound even where the aggregate norm
+    above would not notice it.
 """
 from __future__ import annotations
 
@@ -17,6 +23,8 @@ from oracle import block as ob
 
 OUT_TOL = 2e-2
 GRAD_TOL = 3e-2
+ROW_TOL = 6e-2
+ROW_FLOOR = 0.1
 
 
 def rel_fro(a: torch.Tensor, b: torch.Tensor) -> float:
@@ -33,6 +41,24 @@ def assert_out_close(name: str, got: torch.Tensor, ref: torch.Tensor, tol: float
     assert torch.isfinite(got.float()).all(), f"{name}: non-finite values"
     mr, rf = max_rel(got, ref), rel_fro(got, ref)
     assert mr <= tol and rf <= tol, f"{name}: max-abs/max|ref| = {mr:.3e}, rel-fro = {rf:.3e} (tol {tol})"
+
+
+def assert_rows_close(name: str, got: torch.Tensor, ref: torch.Tensor, tol: float = ROW_TOL,
+                      floor: float = ROW_FLOOR) -> float:
+    """Per-row bound (rows = last dimension); returns the worst ratio."""
+    g = got.detach().double().cpu().reshape(-1, got.shape[-1])
+    r = ref.detach().double().cpu().reshape(-1, ref.shape[-1])
+    assert g.shape == r.shape, (name, tuple(got.shape), tuple(ref.shape))
+    assert torch.isfinite(g).all(), f"{name}: non-finite values"
+    err = (g - r).norm(dim=1)
+    scale = r.norm(dim=1)
+    fl = floor * float(scale.pow(2).mean().sqrt())
+    ratio = err / scale.clamp_min(max(fl, 1e-30))
+    worst = int(ratio.argmax())
+    w = float(ratio[worst])
+    print(f"  rows {name}: worst {w:.3e} at row {worst} of {g.shape[0]}, median {float(ratio.median()):.3e}")
+    assert w <= tol, f"{name}: row {worst} of {g.shape[0]}: error / scale = {w:.3e} (tol {tol})"
+    return w
 
 
 def assert_grad_close(name: str, got: torch.Tensor, ref: torch.Tensor, tol: float = GRAD_TOL,
@@ -70,6 +96,9 @@ def check_block(w: Workload, B: int | None = None, seed: int | None = None, tabl
     assert_out_close("y", got["y"], ref["y"])
     for k in ("dx", "dwq", "dwk", "dwv", "dwg", "dwo"):
         assert_grad_close(k, got[k], ref[k], scale=ref["dwv"])
+    if float(ref["dx"].norm()) > 0:
+        assert_rows_close("y per token", got["y"], ref["y"])
+        assert_rows_close("dx per token", got["dx"], ref["dx"])
     if table_grad:
         T = inp["x"].shape[1]
         assert_grad_close("df1", got["df1"][:T], ref["df1"][:T], scale=ref["dwv"])

@@ -134,9 +134,12 @@ def test_decode_graph_replays_match_eager_steps():
     cache_g = KVCache.empty(B, H, N, cap, "cuda")
     blk.prefill(x[:, :T0], cache_e)
     blk.prefill(x[:, :T0], cache_g)
+    before_k, before_v = cache_g.k.clone(), cache_g.v.clone()
     graph = DecodeGraph(*blk.ws, blk.f1, blk.f2, H, N, cache_g)
-    # The warm-up and capture wrote row 0 of the graph's cache: restore it.
-    blk.prefill(x[:, :T0], cache_g)
+    torch.cuda.synchronize()
+    # Building the graph (warm-up + capture) leaves the prefilled cache untouched.
+    assert torch.equal(cache_g.k, before_k) and torch.equal(cache_g.v, before_v)
+    del before_k, before_v
     for s in range(6):
         pos = [T0 + s, T0 + s, max(0, T0 - 40 + 7 * s)]
         y_e = blk.decode(x[:, T0 + s], pos, cache_e)

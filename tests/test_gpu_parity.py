@@ -158,6 +158,78 @@ def test_deterministic():
         assert torch.equal(a[k], b[k]), k
 
 
+def _module_and_tables(C, H, N, T, scale=1.0, L0=None, seed=21):
+    from memory_efficient_attn_layer_amd.module import CausalSoftmaxAttention
+    from memory_efficient_attn_layer_amd.yarn import Yarn
+
+    torch.manual_seed(seed)
+    m = CausalSoftmaxAttention(C, H, N)
+    with torch.no_grad():  # README.md:35 zeroes o_proj; give it values so every gradient flows
+        m.o_proj.weight.uniform_(-0.5 / math.sqrt(C), 0.5 / math.sqrt(C))
+    m = m.bfloat16().cuda()
+    yarn = Yarn(N, T, scale=scale, original_context=L0, device="cuda")
+    return m, yarn
+
+
+def test_module_forward_backward_matches_oracle():
+    """The drop-in call path: CausalSoftmaxAttention.forward -> fused_attn
+    (README.md:37-68, fast_triton_attn.py:681-697) with Parameters and a Yarn
+    table module, then loss.backward(); every Parameter .grad and x.grad
+    against the oracle."""
+    C, H, N, T = 512, 8, 64, 256
+    m, yarn = _module_and_tables(C, H, N, T, scale=4.0, L0=64)
+    g = torch.Generator().manual_seed(5)
+    x0 = torch.randn(2, T, C, generator=g).bfloat16()
+    dy = torch.randn(2, T, C, generator=g).bfloat16()
+    x = x0.cuda().requires_grad_(True)
+    y = m(x, yarn)
+    assert y.grad_fn is not None
+    (y.float() * dy.cuda().float()).sum().backward()
+    torch.cuda.synchronize()
+    inp = dict(x=x0, wq=m.q_proj.weight, wk=m.k_proj.weight, wv=m.v_proj.weight, wg=m.g_proj.weight,
+               wo=m.o_proj.weight, f1=yarn.factor1, f2=yarn.factor2, dy=dy)
+    ref = ob.block_grads(inp, H, N)
+    assert_out_close("y", y, ref["y"])
+    assert_grad_close("x.grad", x.grad, ref["dx"])
+    for name, k in (("q_proj", "dwq"), ("k_proj", "dwk"), ("v_proj", "dwv"), ("g_proj", "dwg"), ("o_proj", "dwo")):
+        assert_grad_close(f"{name}.weight.grad", getattr(m, name).weight.grad, ref[k])
+    assert yarn.factor1.grad is None  # table buffers receive no gradient
+
+
+@pytest.mark.parametrize("mode", ["no_grad", "inference_mode"])
+def test_module_inference_at_wide_width_saves_nothing(mode):
+    """Inference through the module at the prefill widths (C=2048, H=16,
+    N=128; C > 1024 has no backward): runs, matches the oracle, keeps no
+    graph and allocates no O / lse (the peak stays below what saving them
+    would add to y, the workspace and the fp32 tables)."""
+    from memory_efficient_attn_layer_amd import _lib
+
+    C, H, N, T = 2048, 16, 128, 256
+    m, yarn = _module_and_tables(C, H, N, T, scale=8.0, L0=64)
+    x0 = torch.randn(1, T, C, generator=torch.Generator().manual_seed(9)).bfloat16()
+    x = x0.cuda()
+    ctx = torch.no_grad() if mode == "no_grad" else torch.inference_mode()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    with ctx:
+        y = m(x, yarn)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    assert y.grad_fn is None
+    M, HN = T, H * N
+    d = _lib.desc(1, T, C, H, N, T, 1e-6)
+    ws = _lib.load().mea_workspace_bytes(d, _lib.MEA_PASS_FWD)
+    no_save = M * C * 2 + ws + 2 * T * N * 4
+    saves = M * HN * 2 + H * M * 4
+    assert peak < no_save + saves // 2, (peak, no_save, saves)
+    inp = dict(x=x0, wq=m.q_proj.weight, wk=m.k_proj.weight, wv=m.v_proj.weight, wg=m.g_proj.weight,
+               wo=m.o_proj.weight, f1=yarn.factor1, f2=yarn.factor2)
+    ref = ob.block_forward(*(inp[n].detach().float().cpu() for n in ("x", "wq", "wk", "wv", "wg", "wo", "f1", "f2")),
+                           H, N)
+    assert_out_close("y", y, ref)
+
+
 def test_inference_forward_matches_training_forward():
     inp = make_inputs(W0)
     g = {k: v.cuda() for k, v in inp.items()}

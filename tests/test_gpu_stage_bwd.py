@@ -1,0 +1,91 @@
+"""Per-row parity of the backward's intermediate gradients against the fp32
+oracle (mea_bwd_stage_grads).
+
+The fused backward never materialises dQ, dK or dV on their own: the
+attention-backward kernels hand their rows straight to the exact q/k RMSNorm
++ rotary chain and to the input-RMSNorm row scale. This test checks what
+leaves those kernels, row by row, against the oracle's autograd gradients of
+the same intermediates (oracle.block.block_grads(with_intermediates=True)):
+
+  dO     = dL/dO            (B, H, T, N)   the gate backward's output
+  delta  = rowsum(dO * O)   (B, H, T)      error per row bounded by
+                                           ROW_TOL * |dO_r| |O_r|
+  da_v   = rx * dL/dv       (B, H, T, N)   dV itself, times rx
+  da_q   = rx * dL/da_q     (B, H, T, N)   dQ through the exact chain
+  da_k   = rx * dL/da_k     (B, H, T, N)   dK through the exact chain
+  da_g   = rx * dL/da_g     (B, T, H*N)
+  df1, df2 (T, N)                          the table gradients, per position
+
+rx = 1/rms(x) per token. The chain da = rq (R^T dq - qh (R^T dq . qh) / N)
+is an invertible rotation followed by a projection that removes only the
+component of R^T dq along qh, which nothing downstream depends on; so a row
+of da_q (da_k) checks the whole row of dQ (dK) except that component.
+"""
+import pytest
+import torch
+
+from memory_efficient_attn_layer_amd import stages
+from memory_efficient_attn_layer_amd.synthetic import WORKLOADS, Workload, make_inputs
+from oracle import block as ob
+from tests.parity_util import ROW_TOL, assert_grad_close, assert_rows_close
+
+pytestmark = pytest.mark.gpu
+
+W0, W1 = WORKLOADS[0], WORKLOADS[1]
+NAMES = ("x", "wq", "wk", "wv", "wg", "wo", "f1", "f2")
+
+
+def _w(name, B, T, C, H, N, scale=1.0, L0=None):
+    return Workload(99, name, B, T, C, H, N, scale, L0)
+
+
+CASES = [
+    ("cfg0-full", W0, None),
+    ("cfg1-b1-t4096", W1, 1),
+    ("cfg2-yarn4-b1-t2048", _w("c2", 1, 2048, 512, 8, 64, 4.0, 8192), None),
+    ("cfg3-b1-t1024", _w("c3", 1, 1024, 1024, 8, 128), None),
+    ("ragged-b3-t77", _w("r", 3, 77, 256, 2, 64), None),
+    ("yarn8-b2-t300-n128", _w("y8", 2, 300, 256, 2, 128, 8.0, 64), None),
+    ("h5-hn320-b1-t150", _w("h5", 1, 150, 256, 5, 64), None),
+]
+
+
+@pytest.mark.parametrize("label,w,B", CASES, ids=[c[0] for c in CASES])
+def test_backward_intermediates_per_row(label, w, B):
+    print(f"\n[{label}] B={w.B if B is None else B} T={w.T} C={w.C} H={w.H} N={w.N} yarn={w.yarn_scale}", flush=True)
+    inp = make_inputs(w, B=B)
+    g = {k: v.cuda() for k, v in inp.items()}
+    H, N = w.H, w.N
+    _, o_save, lse = stages.fwd_saved(*(g[n] for n in NAMES), H, N)
+    got = stages.bwd_grads(*(g[n] for n in NAMES), o_save, lse, g["dy"], H, N, table_grad=True)
+    torch.cuda.synchronize()
+
+    ref = ob.block_grads(inp, H, N, dtype=torch.float32, with_intermediates=True)
+    it, ig = ref["inter"], ref["inter_grad"]
+    Bv, T = inp["x"].shape[:2]
+    xf = inp["x"].float()
+    rx = torch.rsqrt(xf.pow(2).mean(-1) + 1e-6)                      # (B, T)
+    rx_h = rx[:, None, :, None]                                        # (B, 1, T, 1)
+
+    def head_major(t):  # (B, T, H, N) or (B, T, H*N) -> (B, H, T, N)
+        return t.reshape(Bv, T, H, N).permute(0, 2, 1, 3)
+
+    dO_ref = head_major(ig["o"])
+    assert_rows_close("dO", got["dO"], dO_ref)
+    o_ref = head_major(it["o"])
+    delta_ref = (dO_ref * o_ref).sum(-1)
+    bound = ROW_TOL * dO_ref.norm(dim=-1) * o_ref.norm(dim=-1) + 1e-30
+    derr = (got["delta"].double().cpu() - delta_ref.double()).abs()
+    worst = float((derr / bound.double()).max())
+    print(f"  rows delta: worst {worst * ROW_TOL:.3e} of |dO||O|", flush=True)
+    assert worst <= 1.0, f"delta: worst error / (tol |dO||O|) = {worst:.3e}"
+
+    assert_rows_close("da_v (dV)", got["dav"], rx_h * head_major(ig["a_v"]))
+    assert_rows_close("da_q (dQ chain)", got["daq"], rx_h * head_major(ig["a_q"]))
+    assert_rows_close("da_k (dK chain)", got["dak"], rx_h * head_major(ig["a_k"]))
+    assert_rows_close("da_g", got["dag"], rx[:, :, None] * ig["a_g"])
+    assert_grad_close("df1", got["df1"][:T], ref["df1"][:T])
+    assert_grad_close("df2", got["df2"][:T], ref["df2"][:T])
+    assert_rows_close("df1 per position", got["df1"][:T], ref["df1"][:T])
+    assert_rows_close("df2 per position", got["df2"][:T], ref["df2"][:T])
+

@@ -222,3 +222,24 @@ def test_module_and_tables_construct_on_cpu():
     x = torch.randn(1, 8, 256, dtype=torch.bfloat16)
     with pytest.raises(TypeError):  # fp32 weights of a fresh nn.Linear are rejected like the reference would
         fused_attn(x, m.q_proj, m.k_proj, m.v_proj, m.g_proj, m.o_proj, y, 4, 64)
+
+
+def test_save_decision_follows_grad_mode():
+    """Whether the forward saves activations (and so needs the backward's
+    width limit, C <= 1024) is decided from grad mode and requires_grad
+    before Function.forward runs: under no_grad / inference_mode a module
+    with C = 2048 gets past validation to the device check (no GPU here),
+    while with grad enabled it is refused for its width."""
+    m = CausalSoftmaxAttention(2048, 16, 128).bfloat16()
+    y = Yarn(128, 16)
+    x = torch.randn(1, 16, 2048, dtype=torch.bfloat16)
+    for ctx in (torch.no_grad, torch.inference_mode):
+        with ctx(), pytest.raises(RuntimeError, match="ROCm GPU"):
+            m(x, y)
+    with pytest.raises(ValueError, match="backward supports"):
+        m(x, y)
+    # Nothing requires grad: no save even with grad mode on.
+    for p in m.parameters():
+        p.requires_grad_(False)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        m(x, y)
