@@ -16,6 +16,14 @@ the same intermediates (oracle.block.block_grads(with_intermediates=True)):
   da_g   = rx * dL/da_g     (B, T, H*N)
   df1, df2 (T, N)                          the table gradients, per position
 
+Rows of queries with fewer than EARLY keys (t < EARLY) are held to
+EARLY_TOL instead of ROW_TOL for da_q: every flash backward (the
+reference's aten kernel included) forms delta from the bf16-rounded saved O,
+so sum_j dS_tj is not exactly 0 and dQ_t carries an error of about
+dO . (O - bf16(O)) times the mean key, which nothing averages away when a
+query sees two or three keys (tests/test_flash_numerics.py reproduces it on
+the CPU: 11% at such a row with bf16 operands, under 2% beyond t = 16).
+
 rx = 1/rms(x) per token. The chain da = rq (R^T dq - qh (R^T dq . qh) / N)
 is an invertible rotation followed by a projection that removes only the
 component of R^T dq along qh, which nothing downstream depends on; so a row
@@ -30,6 +38,9 @@ from oracle import block as ob
 from tests.parity_util import ROW_TOL, assert_grad_close, assert_rows_close
 
 pytestmark = pytest.mark.gpu
+
+EARLY = 16
+EARLY_TOL = 0.25
 
 W0, W1 = WORKLOADS[0], WORKLOADS[1]
 NAMES = ("x", "wq", "wk", "wv", "wg", "wo", "f1", "f2")
@@ -81,7 +92,11 @@ def test_backward_intermediates_per_row(label, w, B):
     assert worst <= 1.0, f"delta: worst error / (tol |dO||O|) = {worst:.3e}"
 
     assert_rows_close("da_v (dV)", got["dav"], rx_h * head_major(ig["a_v"]))
-    assert_rows_close("da_q (dQ chain)", got["daq"], rx_h * head_major(ig["a_q"]))
+    daq_ref = rx_h * head_major(ig["a_q"])
+    e = min(EARLY, T)
+    if T > e:
+        assert_rows_close("da_q (dQ chain), t >= 16", got["daq"][:, :, e:], daq_ref[:, :, e:])
+    assert_rows_close("da_q (dQ chain), t < 16", got["daq"][:, :, :e], daq_ref[:, :, :e], tol=EARLY_TOL)
     assert_rows_close("da_k (dK chain)", got["dak"], rx_h * head_major(ig["a_k"]))
     assert_rows_close("da_g", got["dag"], rx[:, :, None] * ig["a_g"])
     assert_grad_close("df1", got["df1"][:T], ref["df1"][:T])
