@@ -16,7 +16,9 @@
  *
  * Conventions shared by every entry point:
  *   - All device pointers are borrowed; the library never allocates device
- *     memory. Outputs and the workspace are allocated by the caller.
+ *     memory. Outputs and the workspace are allocated by the caller
+ *     (mea_decode_static takes no workspace: it uses a static buffer of the
+ *     library instead).
  *   - Activations and weights are bf16 (the only dtype the reference runs
  *     with, fast_triton_attn.py:32,103,123). Rotary tables, lse and the
  *     per-row statistics are fp32.
@@ -64,8 +66,13 @@ enum {
   MEA_ERR_ALIGN = -6,       /* a pointer is not 16-byte aligned */
   MEA_ERR_EPS = -7,         /* eps not finite and positive */
   MEA_ERR_LAUNCH = -8,      /* HIP reported an error at launch */
-  MEA_ERR_ALIAS = -9        /* dx overlaps another argument of mea_bwd */
+  MEA_ERR_ALIAS = -9,       /* dx overlaps another argument of mea_bwd */
+  MEA_ERR_SCRATCH = -10,    /* shape needs more than MEA_STATIC_SCRATCH_BYTES */
+  MEA_ERR_DEVICE = -11      /* no current device, or the stream is another device's */
 };
+
+/* Size of the static scratch buffer of mea_decode_static (per GPU). */
+#define MEA_STATIC_SCRATCH_BYTES (16u << 20)
 
 /* Which pass a workspace size is asked for. */
 enum { MEA_PASS_FWD = 0, MEA_PASS_BWD = 1 };
@@ -201,6 +208,31 @@ int mea_decode(const mea_desc* d, const void* x, const void* wq,
                const float* f1, const float* f2, const int32_t* pos,
                void* k_cache, void* v_cache, void* y, void* ws,
                size_t ws_bytes, void* stream);
+
+/*
+ * mea_decode without a workspace argument: the step's scratch (the new
+ * tokens' projections, q/k/v/gate rows and the split-attention partials,
+ * mea_decode_workspace_bytes(d) bytes) lives in a static device buffer of
+ * MEA_STATIC_SCRATCH_BYTES inside the library, so a call allocates nothing
+ * and needs no caller-provided scratch. No counterpart in the reference; it
+ * is for callers that cannot allocate device memory: serving loops with a
+ * fixed memory budget, code under graph capture, harnesses that forbid
+ * allocation. Shapes whose scratch exceeds the buffer return
+ * MEA_ERR_SCRATCH (16 MiB covers, e.g., B * H * N * C up to ~10^9 with
+ * 4H*N*B*4 bytes of projections; mea_decode_workspace_bytes tells).
+ *
+ * Runs on the calling thread's current device, which must be the stream's
+ * (else MEA_ERR_DEVICE); the buffer's address on each device is looked up
+ * on the first call there. Every call on one GPU shares that GPU's buffer:
+ * calls that may overlap in time on one GPU (different streams, or threads
+ * without ordering) race and must be serialised by the caller. Arguments
+ * and results otherwise exactly as mea_decode.
+ */
+int mea_decode_static(const mea_desc* d, const void* x, const void* wq,
+                      const void* wk, const void* wv, const void* wg,
+                      const void* wo, const float* f1, const float* f2,
+                      const int32_t* pos, void* k_cache, void* v_cache,
+                      void* y, void* stream);
 
 /*
  * Stage: input RMSNorm + q/k/v/g projection + per-head q/k RMSNorm + rotary +

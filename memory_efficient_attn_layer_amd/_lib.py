@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libmea.so")
 
 MEA_PASS_FWD = 0
 MEA_PASS_BWD = 1
+MEA_STATIC_SCRATCH_BYTES = 16 << 20  # include/mea.h
 
 
 class MeaDesc(ctypes.Structure):
@@ -58,6 +59,7 @@ EXPORTS = {
     "mea_prefill": (ctypes.c_int, [_desc] + [_vp] * 6 + [_fp, _fp, _vp, _vp, _vp, ctypes.c_int64, _vp, ctypes.c_size_t, _vp]),
     "mea_decode_workspace_bytes": (ctypes.c_size_t, [_desc]),
     "mea_decode": (ctypes.c_int, [_desc] + [_vp] * 6 + [_fp, _fp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "mea_decode_static": (ctypes.c_int, [_desc] + [_vp] * 6 + [_fp, _fp, _vp, _vp, _vp, _vp, _vp]),
     "mea_qkvg_proj": (ctypes.c_int, [_desc] + [_vp] * 5 + [_fp, _fp] + [_vp] * 4 + [_fp, _fp, _fp, _vp]),
     "mea_attn_fwd": (ctypes.c_int, [_desc, _vp, _vp, _vp, _vp, _fp, _vp]),
     "mea_gate_oproj": (ctypes.c_int, [_desc, _vp, _vp, _vp, _vp, _vp]),

@@ -666,17 +666,28 @@ size_t mea_decode_workspace_bytes(const mea_desc* d) {
   return make_dec_layout(*d).total;
 }
 
-int mea_decode(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
-               const void* wo, const float* f1, const float* f2, const int32_t* pos, void* k_cache, void* v_cache,
-               void* y, void* ws, size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Argument checks of the decode step (everything but the scratch memory).
+int decode_check(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+                 const void* wo, const float* f1, const float* f2, const int32_t* pos, void* k_cache, void* v_cache,
+                 void* y) {
   int rc = validate(d, MEA_PASS_FWD);
   if (rc != MEA_OK) return rc;
-  rc = check_ptrs({x, wq, wk, wv, wg, wo, f1, f2, k_cache, v_cache, y, ws});
+  rc = check_ptrs({x, wq, wk, wv, wg, wo, f1, f2, k_cache, v_cache, y});
   if (rc != MEA_OK) return rc;
   if (pos == nullptr) return MEA_ERR_NULL;
   if (((uintptr_t)pos & 3u) != 0) return MEA_ERR_ALIGN;
+  return MEA_OK;
+}
+
+// The decode step's launches; ws holds make_dec_layout(*d).total bytes.
+int decode_launch(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+                  const void* wo, const float* f1, const float* f2, const int32_t* pos, void* k_cache, void* v_cache,
+                  void* y, void* ws, void* stream) {
   const DecLayout L = make_dec_layout(*d);
-  if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
   const int N = (int)d->N, B = (int)d->B, C = (int)d->C, HN = (int)(d->H * d->N);
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* a = at<float>(ws, L.a);
@@ -753,6 +764,65 @@ int mea_decode(const mea_desc* d, const void* x, const void* wq, const void* wk,
   return MEA_OK;
 }
 
+// Scratch of mea_decode_static: a file-scope device array, one copy per GPU
+// (each GPU the library runs on holds it until the process ends). In host
+// code `scratch` is only a handle: its device address on the current GPU
+// comes from hipGetSymbolAddress, looked up once per device and kept in
+// g_scratch_addr, and only that address is handed to kernels.
+__device__ __attribute__((aligned(256))) unsigned char scratch[MEA_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (the stream's device).
+int static_scratch(void* stream, void** addr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MEA_ERR_DEVICE;
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess || sdev != dev)
+      return MEA_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return MEA_ERR_DEVICE;
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return MEA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mea_decode(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
+               const void* wo, const float* f1, const float* f2, const int32_t* pos, void* k_cache, void* v_cache,
+               void* y, void* ws, size_t ws_bytes, void* stream) {
+  int rc = decode_check(d, x, wq, wk, wv, wg, wo, f1, f2, pos, k_cache, v_cache, y);
+  if (rc != MEA_OK) return rc;
+  rc = check_ptrs({ws});
+  if (rc != MEA_OK) return rc;
+  if (ws_bytes < make_dec_layout(*d).total) return MEA_ERR_WORKSPACE;
+  return decode_launch(d, x, wq, wk, wv, wg, wo, f1, f2, pos, k_cache, v_cache, y, ws, stream);
+}
+
+int mea_decode_static(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv,
+                      const void* wg, const void* wo, const float* f1, const float* f2, const int32_t* pos,
+                      void* k_cache, void* v_cache, void* y, void* stream) {
+  int rc = decode_check(d, x, wq, wk, wv, wg, wo, f1, f2, pos, k_cache, v_cache, y);
+  if (rc != MEA_OK) return rc;
+  // Every scratch byte the step reads is written by the step first, so the
+  // previous call's contents need no clearing.
+  if (make_dec_layout(*d).total > (size_t)MEA_STATIC_SCRATCH_BYTES) return MEA_ERR_SCRATCH;
+  void* ws = nullptr;
+  rc = static_scratch(stream, &ws);
+  if (rc != MEA_OK) return rc;
+  return decode_launch(d, x, wq, wk, wv, wg, wo, f1, f2, pos, k_cache, v_cache, y, ws, stream);
+}
+
 const char* mea_strerror(int code) {
   switch (code) {
     case MEA_OK: return "ok";
@@ -765,6 +835,8 @@ const char* mea_strerror(int code) {
     case MEA_ERR_EPS: return "eps must be finite and positive";
     case MEA_ERR_LAUNCH: return "HIP kernel launch failed";
     case MEA_ERR_ALIAS: return "dx overlaps another argument of the backward";
+    case MEA_ERR_SCRATCH: return "the decode step needs more scratch than mea_decode_static's static buffer";
+    case MEA_ERR_DEVICE: return "no current device, or the stream belongs to another device";
     default: return "unknown status";
   }
 }

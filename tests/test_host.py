@@ -44,7 +44,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_strerror_and_version(lib):
-    for code in range(0, -9, -1):
+    for code in range(0, -12, -1):
         msg = _lib.strerror(code)
         assert msg and msg != "unknown status", code
     assert _lib.strerror(-1234) == "unknown status"
@@ -243,3 +243,20 @@ def test_save_decision_follows_grad_mode():
         p.requires_grad_(False)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         m(x, y)
+
+
+def test_static_decode_validation(lib):
+    """mea_decode_static checks its arguments, then refuses a shape whose
+    scratch exceeds the static buffer, before touching the device."""
+    fake = 1 << 20  # aligned, never dereferenced: validation fails first
+    dargs = [fake] * 12  # x wq wk wv wg wo f1 f2 pos k_cache v_cache y
+    d = _d(T=512, T_max=512)
+    no_pos = list(dargs)
+    no_pos[8] = None
+    assert lib.mea_decode_static(ctypes.byref(d), *no_pos, None) == _header_enum("MEA_ERR_NULL")
+    assert lib.mea_decode_static(ctypes.byref(_d(N=96)), *dargs, None) == _header_enum("MEA_ERR_HEAD_DIM")
+    big = _d(B=4096, T=512, T_max=512, C=2048, H=16, N=128)
+    assert lib.mea_decode_workspace_bytes(ctypes.byref(big)) > _lib.MEA_STATIC_SCRATCH_BYTES
+    assert lib.mea_decode_static(ctypes.byref(big), *dargs, None) == _header_enum("MEA_ERR_SCRATCH")
+    m = re.search(r"#define MEA_STATIC_SCRATCH_BYTES \((\d+)u << (\d+)\)", HEADER.read_text())
+    assert int(m.group(1)) << int(m.group(2)) == _lib.MEA_STATIC_SCRATCH_BYTES
