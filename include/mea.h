@@ -74,11 +74,14 @@ enum {
 /* Size of the static scratch buffer of mea_decode_static (per GPU). */
 #define MEA_STATIC_SCRATCH_BYTES (16u << 20)
 
-/* Which pass a workspace size is asked for. */
-enum { MEA_PASS_FWD = 0, MEA_PASS_BWD = 1 };
+/* Which pass a workspace size is asked for: the forward, the backward, or a
+ * backward that also writes the table gradients df1 / df2 (it needs
+ * B * T * N * 8 more bytes for per-token partial sums). */
+enum { MEA_PASS_FWD = 0, MEA_PASS_BWD = 1, MEA_PASS_BWD_TABLES = 2 };
 
 /*
- * Workspace bytes needed by mea_fwd (pass 0) or mea_bwd (pass 1).
+ * Workspace bytes needed by mea_fwd (pass 0), mea_bwd (pass 1) or mea_bwd
+ * with table gradients (pass 2).
  * Returns 0 when the descriptor is invalid.
  * Replaces the torch.empty transients of FusedAttentionFunction.forward
  * (fast_triton_attn.py:381,391-394,447) and .backward (:505-506,518-524,560).
@@ -118,7 +121,11 @@ int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk,
  *   dwq, dwk, dwv, dwg  (H*N, C) bf16      out
  *   dwo                 (C, H*N) bf16      out
  *   df1, df2            (T_max, N) fp32    out, rows 0..T-1 written; both may
- *                                          be NULL to skip the table gradient
+ *                                          be NULL to skip the table gradient.
+ *                                          Given, they need the workspace of
+ *                                          MEA_PASS_BWD_TABLES; the sum over
+ *                                          batch and heads runs in a fixed
+ *                                          order (deterministic)
  *
  * dx also holds the gradient of the gate projection's output (rows of H*N
  * values at stride C) until the last kernel overwrites it with the result,

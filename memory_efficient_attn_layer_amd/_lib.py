@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libmea.so")
 
 MEA_PASS_FWD = 0
 MEA_PASS_BWD = 1
+MEA_PASS_BWD_TABLES = 2  # backward that also writes the table gradients
 MEA_STATIC_SCRATCH_BYTES = 16 << 20  # include/mea.h
 
 

@@ -150,7 +150,7 @@ class FusedAttentionFunction(torch.autograd.Function):
             df2 = torch.empty((T, N), device=dev, dtype=torch.float32)
         else:
             df1 = df2 = None
-        ws_bytes = lib.mea_workspace_bytes(d, _lib.MEA_PASS_BWD)
+        ws_bytes = lib.mea_workspace_bytes(d, _lib.MEA_PASS_BWD_TABLES if want_f else _lib.MEA_PASS_BWD)
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
         with torch.cuda.device(dev):
             rc = lib.mea_bwd(
@@ -272,7 +272,7 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
             df2 = torch.empty((max_len, N), device=dev, dtype=torch.float32)
         else:
             df1 = df2 = None
-        ws_bytes = lib.mea_workspace_bytes(d_ws, _lib.MEA_PASS_BWD)
+        ws_bytes = lib.mea_workspace_bytes(d_ws, _lib.MEA_PASS_BWD_TABLES if want_f else _lib.MEA_PASS_BWD)
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
         with torch.cuda.device(dev):
             rc = lib.mea_bwd_varlen(

@@ -22,6 +22,7 @@ struct Layout {
   size_t q, k, v, sig, tpos, o, qkn;         // forward (tpos: packed sequences only)
   size_t dO, daq, dag;                       // backward (da_k, da_v overwrite k, v)
   size_t rx, rq, rk, delta, woT, wcatT, part;
+  size_t tpart;                              // table-gradient partials (MEA_PASS_BWD_TABLES)
   size_t total;
 };
 
@@ -51,6 +52,7 @@ Layout make_layout(const mea_desc& d, int pass) {
     L.woT = take(HN * C * 2);
     L.wcatT = take(C * 4 * HN * 2);
     L.part = take((size_t)mea::dw_splits((int)M, (int)C, (int)HN) * (4 * HN * C + C * HN) * 4);
+    if (pass == MEA_PASS_BWD_TABLES) L.tpart = take(M * 2 * (size_t)d.N * 4);
   }
   L.total = off;
   return L;
@@ -61,7 +63,8 @@ int validate(const mea_desc* d, int pass) {
   if (d->B < 1 || d->T < 1 || d->H < 1 || d->T_max < d->T) return MEA_ERR_SHAPE;
   if (d->N != 64 && d->N != 128) return MEA_ERR_HEAD_DIM;
   if (d->C < 256 || d->C % 256 != 0) return MEA_ERR_MODEL_DIM;
-  if (pass == MEA_PASS_BWD && d->C > 1024) return MEA_ERR_MODEL_DIM;
+  const bool bwd = pass == MEA_PASS_BWD || pass == MEA_PASS_BWD_TABLES;
+  if (bwd && d->C > 1024) return MEA_ERR_MODEL_DIM;
   if (pass == MEA_PASS_FWD && d->C > 4096) return MEA_ERR_MODEL_DIM;
   if (!(d->eps > 0.f) || !isfinite(d->eps)) return MEA_ERR_EPS;
   // All row and element indices used by the kernels fit in 31 bits.
@@ -71,7 +74,7 @@ int validate(const mea_desc* d, int pass) {
     return MEA_ERR_SHAPE;
   // The backward GEMMs address a head-major gradient with 32-bit byte
   // offsets spanning up to one head of one batch plus a few hundred rows.
-  if (pass == MEA_PASS_BWD && d->H * (d->T + 256) * d->N >= (INT64_C(1) << 30)) return MEA_ERR_SHAPE;
+  if (bwd && d->H * (d->T + 256) * d->N >= (INT64_C(1) << 30)) return MEA_ERR_SHAPE;
   return MEA_OK;
 }
 
@@ -130,12 +133,12 @@ T* at(void* ws, size_t off) {
 enum KernelId {
   K_QKVG_PROJ, K_ATTN_FWD, K_GATE_OPROJ, K_TRANSPOSE, K_ZERO, K_DZ_GATE_BWD,
   K_ATTN_BWD_DQ, K_ATTN_BWD_DKDV, K_DW_PARTIAL, K_DW_REDUCE, K_DX,
-  K_KV_APPEND, K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_COUNT
+  K_KV_APPEND, K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_REDUCE, K_COUNT
 };
 const char* const kKernelNames[K_COUNT] = {
     "qkvg_proj", "attn_fwd", "gate_oproj", "transpose", "zero_f32", "dz_gate_bwd",
     "attn_bwd_dq", "attn_bwd_dkdv", "dw_partial", "dw_reduce", "dx",
-    "kv_append", "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj"};
+    "kv_append", "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad_reduce"};
 
 struct ProfRec {
   int kernel;
@@ -180,7 +183,7 @@ hipError_t timed(int kernel, hipStream_t s, F launch) {
 extern "C" {
 
 size_t mea_workspace_bytes(const mea_desc* d, int pass) {
-  if (pass != MEA_PASS_FWD && pass != MEA_PASS_BWD) return 0;
+  if (pass != MEA_PASS_FWD && pass != MEA_PASS_BWD && pass != MEA_PASS_BWD_TABLES) return 0;
   if (validate(d, pass) != MEA_OK) return 0;
   return make_layout(*d, pass).total;
 }
@@ -388,7 +391,7 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = (int)(d->B * d->T), T = (int)d->T, H = (int)d->H, N = (int)d->N, C = (int)d->C;
   const int HN = H * N;
-  const Layout L = make_layout(*d, MEA_PASS_BWD);
+  const Layout L = make_layout(*d, df1 != nullptr ? MEA_PASS_BWD_TABLES : MEA_PASS_BWD);
 
   // Weight transposes (k-contiguous B operands for dZ and dx).
   MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_transpose(static_cast<const bf16_bits*>(wo), C, HN, HN, bf.woT, C, 0, s); }));
@@ -397,13 +400,6 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
     MEA_TRY(timed(K_TRANSPOSE, s, [&] {
       return mea::launch_transpose(static_cast<const bf16_bits*>(wp[j]), HN, C, C, bf.wcatT, 4 * HN, j * HN, s);
     }));
-  if (df1 != nullptr) {
-    // Table rows the block touches: positions 0 .. T-1 (packed: max_len - 1).
-    const size_t rows = (size_t)(var != nullptr ? var->max_len : T);
-    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df1, rows * N, s); }));
-    MEA_TRY(timed(K_ZERO, s, [&] { return mea::launch_zero_f32(df2, rows * N, s); }));
-  }
-
   // Recompute q, k, v, sigmoid(g) and the three RMS statistics.
   const float qs = q_log2_scale(N);
   int* tpos = nullptr;
@@ -447,8 +443,8 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
   ab.daq = bf.daq;
   ab.dak = bf.k;
   ab.dav = bf.v;
-  ab.df1 = df1;
-  ab.df2 = df2;
+  // Table gradients: per-token partials, summed over the sequences below.
+  ab.tpart = df1 != nullptr ? at<float>(ws, L.tpart) : nullptr;
   ab.B = (int)d->B;
   ab.H = H;
   ab.T = T;
@@ -460,6 +456,11 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
   ab.max_len = var != nullptr ? var->max_len : 0;
   MEA_TRY(timed(K_ATTN_BWD_DQ, s, [&] { return mea::launch_attn_bwd_dq(ab, N, s); }));
   MEA_TRY(timed(K_ATTN_BWD_DKDV, s, [&] { return mea::launch_attn_bwd_dkdv(ab, N, s); }));
+  if (df1 != nullptr) {
+    // Table rows the block touches: positions 0 .. T-1 (packed: max_len - 1).
+    const int rows = var != nullptr ? var->max_len : T;
+    MEA_TRY(timed(K_TABLE_REDUCE, s, [&] { return mea::launch_table_grad_reduce(ab, N, rows, df1, df2, s); }));
+  }
   return MEA_OK;
 }
 
@@ -494,7 +495,7 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
     for (const auto& o : others)
       if (overlaps(dx, act_c, o.first, o.second)) return MEA_ERR_ALIAS;
   }
-  const Layout L = make_layout(*d, MEA_PASS_BWD);
+  const Layout L = make_layout(*d, df1 != nullptr ? MEA_PASS_BWD_TABLES : MEA_PASS_BWD);
   if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = (int)(d->B * d->T), T = (int)d->T, H = (int)d->H, N = (int)d->N, C = (int)d->C;
@@ -590,7 +591,7 @@ int mea_bwd_stage_grads(const mea_desc* d, const void* dy, const void* x, const 
   int rc = bwd_check(d, nullptr, {dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, daq, dak, dav, dag, dO, delta, ws},
                      df1, df2);
   if (rc != MEA_OK) return rc;
-  const Layout L = make_layout(*d, MEA_PASS_BWD);
+  const Layout L = make_layout(*d, df1 != nullptr ? MEA_PASS_BWD_TABLES : MEA_PASS_BWD);
   if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
   const int HN = (int)(d->H * d->N);
   // da_g goes straight to the caller's buffer (token-major rows of H*N).

@@ -9,7 +9,8 @@
 //   q = R qh with R the per-pair block [[f1[2i], f2[2i]], [f2[2i+1], f1[2i+1]]]
 //   dqh = R^T dq
 //   da_q = rq * (dqh - qh * (dqh . qh) / N)
-//   df1[t, n] += dq[n] qh[n],  df2[t, n] += dq[n] qh[n^1]
+//   dF1[t, n] += dq[n] qh[n],  dF2[t, n] += dq[n] qh[n^1]   (summed over
+//   batch and heads: per-token partials, then a reduce over sequences)
 // qh is recovered from the stored rotated q by inverting R per pair, so the
 // recompute pass does not have to keep the pre-rotation values.
 //
@@ -38,11 +39,15 @@ namespace mea {
 // scaled by rx[tok_row0 + t]. out may be xrot itself: every lane writes only
 // the 16 bytes it has read, after reading them, and rows past T are not
 // written.
-template <int N>
+// TG (rotary rows): the table-gradient products of the row go to
+// p.tpart[tok_row0 + t]: written when tg_first, else added. The same lane
+// handles the same 8 columns of a row in every call, so the read-modify-write
+// needs no synchronisation across calls of one workgroup.
+template <int N, bool TG = false>
 __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, const AttnBwdParams& p, int T,
                                              size_t tok_row0, size_t head_row0, bool rotary,
                                              const bf16_bits* xrot, float xscale, const float* rstat,
-                                             bf16_bits* out) {
+                                             bf16_bits* out, bool tg_first = false) {
   constexpr int CPR = N / 8, RPP = 64 / CPR;
   constexpr int NP = 32 / RPP, PB = 2;  // passes; passes whose global operands are fetched together
   static_assert(NP % PB == 0, "pass batches");
@@ -116,13 +121,28 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
         const float sc = rxv * rr, cf = dot / (float)N;
 #pragma unroll
         for (int i = 0; i < 8; ++i) res[i] = sc * (dh[i] - xh[i] * cf);
-        if (p.df1 != nullptr && valid) {
-          float* d1 = p.df1 + (size_t)t * N + dc * 8;
-          float* d2 = p.df2 + (size_t)t * N + dc * 8;
+        if (TG && valid) {
+          float* d1 = p.tpart + (tok_row0 + t) * (2 * N) + dc * 8;
+          float* d2 = d1 + N;
+          f32x4 u[2], w[2];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            atomicAdd(d1 + i, dv[i] * xh[i]);
-            atomicAdd(d2 + i, dv[i] * xh[i ^ 1]);
+          for (int e = 0; e < 4; ++e) {
+            u[0][e] = dv[e] * xh[e];
+            u[1][e] = dv[4 + e] * xh[4 + e];
+            w[0][e] = dv[e] * xh[e ^ 1];
+            w[1][e] = dv[4 + e] * xh[(4 + e) ^ 1];
+          }
+          if (!tg_first) {
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+              u[hf] += *reinterpret_cast<const f32x4*>(d1 + 4 * hf);
+              w[hf] += *reinterpret_cast<const f32x4*>(d2 + 4 * hf);
+            }
+          }
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            *reinterpret_cast<f32x4*>(d1 + 4 * hf) = u[hf];
+            *reinterpret_cast<f32x4*>(d2 + 4 * hf) = w[hf];
           }
         }
       } else {
@@ -155,8 +175,8 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // For N = 64 three workgroups share a CU (164 registers): 64 queries per wave
 // (two blocks sharing every K/V fragment) held two per SIMD ran 4.4% slower.
 // ---------------------------------------------------------------------------
-template <int N, bool VARLEN>
-__global__ __launch_bounds__(256, N == 64 ? 3 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
+template <int N, bool VARLEN, bool TG>
+__global__ __launch_bounds__(256, N == 64 && !TG ? 3 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   constexpr int QW = 32;                 // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
   constexpr int BQ = 4 * QW;             // queries per workgroup
@@ -174,205 +194,215 @@ __global__ __launch_bounds__(256, N == 64 ? 3 : 2) void attn_bwd_dq_kernel(AttnB
 
   // Each XCD walks whole heads (heaviest query block first), so the K/V
   // tiles of a head are fetched once into that XCD's L2. VARLEN: packed
-  // sequences (p.cu), rows relative to the sequence's first token.
-  int T, bh, qi, b, hd;
-  size_t head_row0, tok_row0;
+  // sequences (p.cu), rows relative to the sequence's first token. TG: a
+  // workgroup covers every head of its (sequence, query block), one after
+  // the other, so each token's table-gradient row has a single writer.
+  int T, qi, b, h_first;
+  size_t hrow_base, hrow_step, tok_row0;  // head hd's rows start at hrow_base + hd * hrow_step
+  const int nh = TG ? 1 : p.H;            // heads per grid row
   if constexpr (!VARLEN) {
     T = p.T;
     const int nqb = (T + BQ - 1) / BQ;
-    const int lid = xcd_remap(blockIdx.x, p.B * p.H * nqb);
-    bh = lid / nqb;
+    const int lid = xcd_remap(blockIdx.x, p.B * nh * nqb);
+    const int bh = lid / nqb;
     qi = nqb - 1 - lid % nqb;
-    b = bh / p.H;
-    hd = bh % p.H;
-    head_row0 = (size_t)bh * T;
+    b = bh / nh;
+    h_first = bh % nh;
+    hrow_base = (size_t)b * p.H * T;
+    hrow_step = (size_t)T;
     tok_row0 = (size_t)b * T;
   } else {
     const int nqb = (p.max_len + BQ - 1) / BQ;
-    const int lid = xcd_remap(blockIdx.x, p.nseq * p.H * nqb);
-    bh = lid / nqb;
+    const int lid = xcd_remap(blockIdx.x, p.nseq * nh * nqb);
+    const int bh = lid / nqb;
     qi = nqb - 1 - lid % nqb;
-    b = bh / p.H;
-    hd = bh % p.H;
+    b = bh / nh;
+    h_first = bh % nh;
     // Offsets clamped to [0, total]: a malformed list cannot index outside.
     const int start = min(max(p.cu[b], 0), p.T);
     T = min(max(p.cu[b + 1], start), p.T) - start;
-    head_row0 = (size_t)hd * p.T + start;
+    hrow_base = (size_t)start;
+    hrow_step = (size_t)p.T;
     tok_row0 = (size_t)start;
     if (qi * BQ >= T) return;  // past this sequence's end: uniform, before any barrier
   }
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & 31, h = lane >> 5;
-  const int q0w = qi * BQ + wave * QW;
-  const int kv_end = min(T, qi * BQ + BQ);
-  const size_t head_off = head_row0 * N;
-  const bf16_bits* kg = p.k + head_off;
-  const bf16_bits* vg = p.v + head_off;
+  const int h_end = TG ? p.H : h_first + 1;
+  for (int hd = h_first; hd < h_end; ++hd) {
+    const size_t head_row0 = hrow_base + (size_t)hd * hrow_step;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, h = lane >> 5;
+    const int q0w = qi * BQ + wave * QW;
+    const int kv_end = min(T, qi * BQ + BQ);
+    const size_t head_off = head_row0 * N;
+    const bf16_bits* kg = p.k + head_off;
+    const bf16_bits* vg = p.v + head_off;
 
-  // q^T and dO^T fragments (B operands), and the statistic k-block of the
-  // lane's query q0w + 32qb + c: (-lse*log2e, -delta) in elements 0..5 of the
-  // lanes with h == 0 (zero in the others), kept in a wave-private LDS area
-  // the loop does not touch and matched by the selectors sel_s (S) and sel_d
-  // (dP). The selectors may be the same in every lane, which keeps them
-  // plain constants.
-  bf16x8 qf[QB][KS], df[QB][KS];
-  u32x4* stat = reinterpret_cast<u32x4*>(smem_raw + SM_LOOP) + wave * QB * 64;
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int t = min(q0w + 32 * qb + c, T - 1);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const size_t off = head_off + (size_t)t * N + 16 * ks + 8 * h;
-      qf[qb][ks] = as_frag(ld16(p.q + off));
-      df[qb][ks] = as_frag(ld16(p.dO + off));
-    }
-    const u32x4 sw = stat_pack(-p.lse[head_row0 + t] * kLog2e, -p.delta[head_row0 + t]);
-    stat[qb * 64 + lane] = h == 0 ? sw : u32x4{0u, 0u, 0u, 0u};
-  }
-  const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
-
-  auto issue_tile = [&](int j0, int stage) {
-    bf16_bits* kt = smem + stage * 2 * TILE;
-#pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int slot = (u * 4 + wave) * 64 + lane;
-      const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
-      const size_t off = (size_t)min(j0 + row, T - 1) * N + cc * 8;
-      g2lds16(kg + off, kt + (u * 4 + wave) * 512);
-      g2lds16(vg + off, kt + TILE + (u * 4 + wave) * 512);
-    }
-  };
-
-  f32x16 dq[QB][DB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-    for (int db = 0; db < DB; ++db) dq[qb][db] = zero16();
-
-  // Lane-constant parts of the fragment addresses (elements): a row's
-  // swizzle depends on row & 15 only, so the step and k-step parts of an
-  // address are plain offsets.
-  const int g16 = lane >> 4, i16 = lane & 15;
-  const int tr_row = 4 * h + (i16 >> 2);
-  const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
-  int koff[KS], toff[2][DB];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) koff[ks] = swz_off<CH>(c, 16 * ks + 8 * h);
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int db = 0; db < DB; ++db) toff[x][db] = swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col);
-
-  // One 32-key step of every query block of this wave. MASK: the step
-  // touches the causal diagonal or the end of the sequence.
-  auto step = [&](const bf16_bits* ks_t, const bf16_bits* vs_t, int st, int kb0, auto mask_tag) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    bf16x8 kf[KS], vf[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + st * 32 * N + koff[ks]));
-      vf[ks] = as_frag(*reinterpret_cast<const u32x4*>(vs_t + st * 32 * N + koff[ks]));
-    }
-    bf16x8 sf[QB][2];
+    // q^T and dO^T fragments (B operands), and the statistic k-block of the
+    // lane's query q0w + 32qb + c: (-lse*log2e, -delta) in elements 0..5 of the
+    // lanes with h == 0 (zero in the others), kept in a wave-private LDS area
+    // the loop does not touch and matched by the selectors sel_s (S) and sel_d
+    // (dP). The selectors may be the same in every lane, which keeps them
+    // plain constants.
+    bf16x8 qf[QB][KS], df[QB][KS];
+    u32x4* stat = reinterpret_cast<u32x4*>(smem_raw + SM_LOOP) + wave * QB * 64;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const int qb0 = q0w + 32 * qb;
-      if (MASK && kb0 > qb0 + 31) {
-        sf[qb][0] = sf[qb][1] = as_frag(u32x4{0u, 0u, 0u, 0u});
-        continue;
-      }
-      const bf16x8 stf = as_frag(stat[qb * 64 + lane]);
-      f32x16 s = mfma32(sel_s, stf, zero16()), dp = mfma32(sel_d, stf, zero16());
+      const int t = min(q0w + 32 * qb + c, T - 1);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        s = mfma32(kf[ks], qf[qb][ks], s);
-        dp = mfma32(vf[ks], df[qb][ks], dp);
+        const size_t off = head_off + (size_t)t * N + 16 * ks + 8 * h;
+        qf[qb][ks] = as_frag(ld16(p.q + off));
+        df[qb][ks] = as_frag(ld16(p.dO + off));
       }
-      const int qq = qb0 + c;
+      const u32x4 sw = stat_pack(-p.lse[head_row0 + t] * kLog2e, -p.delta[head_row0 + t]);
+      stat[qb * 64 + lane] = h == 0 ? sw : u32x4{0u, 0u, 0u, 0u};
+    }
+    const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
+
+    auto issue_tile = [&](int j0, int stage) {
+      bf16_bits* kt = smem + stage * 2 * TILE;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float pv = fast_exp2(s[i]);
-        if (MASK) {
-          const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
-          pv = (key > qq || key >= T) ? 0.f : pv;
-        }
-        s[i] = pv * dp[i];
+      for (int u = 0; u < LOADS; ++u) {
+        const int slot = (u * 4 + wave) * 64 + lane;
+        const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+        const size_t off = (size_t)min(j0 + row, T - 1) * N + cc * 8;
+        g2lds16(kg + off, kt + (u * 4 + wave) * 512);
+        g2lds16(vg + off, kt + TILE + (u * 4 + wave) * 512);
       }
+    };
+
+    f32x16 dq[QB][DB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) dq[qb][db] = zero16();
+
+    // Lane-constant parts of the fragment addresses (elements): a row's
+    // swizzle depends on row & 15 only, so the step and k-step parts of an
+    // address are plain offsets.
+    const int g16 = lane >> 4, i16 = lane & 15;
+    const int tr_row = 4 * h + (i16 >> 2);
+    const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+    int koff[KS], toff[2][DB];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) koff[ks] = swz_off<CH>(c, 16 * ks + 8 * h);
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) toff[x][db] = swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col);
+
+    // One 32-key step of every query block of this wave. MASK: the step
+    // touches the causal diagonal or the end of the sequence.
+    auto step = [&](const bf16_bits* ks_t, const bf16_bits* vs_t, int st, int kb0, auto mask_tag) {
+      constexpr bool MASK = decltype(mask_tag)::value;
+      bf16x8 kf[KS], vf[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + st * 32 * N + koff[ks]));
+        vf[ks] = as_frag(*reinterpret_cast<const u32x4*>(vs_t + st * 32 * N + koff[ks]));
+      }
+      bf16x8 sf[QB][2];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int qb0 = q0w + 32 * qb;
+        if (MASK && kb0 > qb0 + 31) {
+          sf[qb][0] = sf[qb][1] = as_frag(u32x4{0u, 0u, 0u, 0u});
+          continue;
+        }
+        const bf16x8 stf = as_frag(stat[qb * 64 + lane]);
+        f32x16 s = mfma32(sel_s, stf, zero16()), dp = mfma32(sel_d, stf, zero16());
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s = mfma32(kf[ks], qf[qb][ks], s);
+          dp = mfma32(vf[ks], df[qb][ks], dp);
+        }
+        const int qq = qb0 + c;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float pv = fast_exp2(s[i]);
+          if (MASK) {
+            const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
+            pv = (key > qq || key >= T) ? 0.f : pv;
+          }
+          s[i] = pv * dp[i];
+        }
+#pragma unroll
+        for (int kst = 0; kst < 2; ++kst) {
+          u32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
+          sf[qb][kst] = as_frag(w);
+        }
+        // Keeps the next query block's S and dP accumulators from going live
+        // before this block's are consumed (they do not fit in registers
+        // together with the resident q, dO and dQ fragments).
+        if (QB > 1) __builtin_amdgcn_sched_barrier(0);
+      }
+      // dQ^T += K^T dS^T, two 16-key MFMA steps.
 #pragma unroll
       for (int kst = 0; kst < 2; ++kst) {
-        u32x4 w;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = pack2(s[8 * kst + 2 * e], s[8 * kst + 2 * e + 1]);
-        sf[qb][kst] = as_frag(w);
-      }
-      // Keeps the next query block's S and dP accumulators from going live
-      // before this block's are consumed (they do not fit in registers
-      // together with the resident q, dO and dQ fragments).
-      if (QB > 1) __builtin_amdgcn_sched_barrier(0);
-    }
-    // dQ^T += K^T dS^T, two 16-key MFMA steps.
+        for (int db = 0; db < DB; ++db) {
+          const bf16_bits* kr = ks_t + (st * 32 + 16 * kst) * N;
+          const bf16x8 kt = frag_from2(lds_read_tr4(kr + toff[0][db]), lds_read_tr4(kr + toff[1][db]));
 #pragma unroll
-    for (int kst = 0; kst < 2; ++kst) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const bf16_bits* kr = ks_t + (st * 32 + 16 * kst) * N;
-        const bf16x8 kt = frag_from2(lds_read_tr4(kr + toff[0][db]), lds_read_tr4(kr + toff[1][db]));
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          if (MASK && kb0 > q0w + 32 * qb + 31) continue;
-          dq[qb][db] = mfma32(kt, sf[qb][kst], dq[qb][db]);
+          for (int qb = 0; qb < QB; ++qb) {
+            if (MASK && kb0 > q0w + 32 * qb + 31) continue;
+            dq[qb][db] = mfma32(kt, sf[qb][kst], dq[qb][db]);
+          }
         }
       }
-    }
-  };
+    };
 
-  const int nkv = (kv_end + BKV - 1) / BKV;
-  // Branch-free loop over the tiles wholly below this wave's first query and
-  // inside the sequence; the split point is per wave (one barrier per tile
-  // in either loop keeps the waves in step).
-  const int nfull = min(nkv, min(q0w + 1, T) / BKV);
-  issue_tile(0, 0);
-  wait_vmcnt0();  // also retires the q/dO fragment loads
-  __syncthreads();
-  int j = 0;
-  for (; j < nfull; ++j) {
-    if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
-    const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
-    step(ks_t, ks_t + TILE, 0, j * BKV, std::false_type{});
-    step(ks_t, ks_t + TILE, 1, j * BKV + 32, std::false_type{});
-    wait_vmcnt0();
+    const int nkv = (kv_end + BKV - 1) / BKV;
+    // Branch-free loop over the tiles wholly below this wave's first query and
+    // inside the sequence; the split point is per wave (one barrier per tile
+    // in either loop keeps the waves in step).
+    const int nfull = min(nkv, min(q0w + 1, T) / BKV);
+    issue_tile(0, 0);
+    wait_vmcnt0();  // also retires the q/dO fragment loads
     __syncthreads();
-  }
-  for (; j < nkv; ++j) {
-    if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
-    const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const int kb0 = j * BKV + st * 32;
-      if (kb0 <= q0w + QW - 1) step(ks_t, ks_t + TILE, st, kb0, std::true_type{});
+    int j = 0;
+    for (; j < nfull; ++j) {
+      if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
+      const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
+      step(ks_t, ks_t + TILE, 0, j * BKV, std::false_type{});
+      step(ks_t, ks_t + TILE, 1, j * BKV + 32, std::false_type{});
+      wait_vmcnt0();
+      __syncthreads();
     }
-    wait_vmcnt0();
-    __syncthreads();
-  }
-
-  // Stage dQ (times the softmax scale) as fp32 rows, then the q chain.
-  float* stg = reinterpret_cast<float*>(smem_raw) + wave * QW * FP;
+    for (; j < nkv; ++j) {
+      if (j + 1 < nkv) issue_tile((j + 1) * BKV, (j + 1) & 1);
+      const bf16_bits* ks_t = smem + (j & 1) * 2 * TILE;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const f32x16& a = dq[qb][db];
-        const f32x4 v = {a[4 * r4], a[4 * r4 + 1], a[4 * r4 + 2], a[4 * r4 + 3]};
-        *reinterpret_cast<f32x4*>(stg + (32 * qb + c) * FP + 32 * db + 8 * r4 + 4 * h) = v * p.scale;
+      for (int st = 0; st < 2; ++st) {
+        const int kb0 = j * BKV + st * 32;
+        if (kb0 <= q0w + QW - 1) step(ks_t, ks_t + TILE, st, kb0, std::true_type{});
       }
-  __syncthreads();
+      wait_vmcnt0();
+      __syncthreads();
+    }
+
+    // Stage dQ (times the softmax scale) as fp32 rows, then the q chain.
+    float* stg = reinterpret_cast<float*>(smem_raw) + wave * QW * FP;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
-    head_row_bwd<N>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, T, tok_row0, head_row0, true, p.q,
-                    1.0f / p.qscale, p.rq, p.daq);
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x16& a = dq[qb][db];
+          const f32x4 v = {a[4 * r4], a[4 * r4 + 1], a[4 * r4 + 2], a[4 * r4 + 3]};
+          *reinterpret_cast<f32x4*>(stg + (32 * qb + c) * FP + 32 * db + 8 * r4 + 4 * h) = v * p.scale;
+        }
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+      head_row_bwd<N, TG>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, T, tok_row0, head_row0, true, p.q,
+                          1.0f / p.qscale, p.rq, p.daq, hd == 0);
+    if (TG) __syncthreads();  // the next head's statistics and tiles reuse the staging area
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -398,8 +428,8 @@ __global__ __launch_bounds__(256, N == 64 ? 3 : 2) void attn_bwd_dq_kernel(AttnB
 // parallelism, ran 7.4% slower. N = 128 runs one wave per SIMD, whose 512
 // registers hold the operands without spilling.
 // ---------------------------------------------------------------------------
-template <int N, bool VARLEN>
-__global__ __launch_bounds__(256, N == 64 ? 3 : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
+template <int N, bool VARLEN, bool TG>
+__global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
   constexpr int KW = 32;                 // keys per wave
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
   static_assert(KB == 1, "one 32-key block per wave");
@@ -422,240 +452,295 @@ __global__ __launch_bounds__(256, N == 64 ? 3 : 1) void attn_bwd_dkdv_kernel(Att
 
   // Each XCD walks whole heads, the key block that sees the most queries
   // first, so the Q/dO tiles of a head are shared in one L2. VARLEN: packed
-  // sequences (p.cu), rows relative to the sequence's first token.
-  int T, bh, ki, b, hd;
-  size_t head_row0, tok_row0;
+  // sequences (p.cu), rows relative to the sequence's first token. TG: a
+  // workgroup covers every head of its (sequence, key block), one after the
+  // other (each token's table-gradient row has a single writer).
+  int T, ki, b, h_first;
+  size_t hrow_base, hrow_step, tok_row0;  // head hd's rows start at hrow_base + hd * hrow_step
+  const int nh = TG ? 1 : p.H;            // heads per grid row
   if constexpr (!VARLEN) {
     T = p.T;
     const int nkb = (T + BKV - 1) / BKV;
-    const int lid = xcd_remap(blockIdx.x, p.B * p.H * nkb);
-    bh = lid / nkb;
+    const int lid = xcd_remap(blockIdx.x, p.B * nh * nkb);
+    const int bh = lid / nkb;
     ki = lid % nkb;
-    b = bh / p.H;
-    hd = bh % p.H;
-    head_row0 = (size_t)bh * T;
+    b = bh / nh;
+    h_first = bh % nh;
+    hrow_base = (size_t)b * p.H * T;
+    hrow_step = (size_t)T;
     tok_row0 = (size_t)b * T;
   } else {
     const int nkb = (p.max_len + BKV - 1) / BKV;
-    const int lid = xcd_remap(blockIdx.x, p.nseq * p.H * nkb);
-    bh = lid / nkb;
+    const int lid = xcd_remap(blockIdx.x, p.nseq * nh * nkb);
+    const int bh = lid / nkb;
     ki = lid % nkb;
-    b = bh / p.H;
-    hd = bh % p.H;
+    b = bh / nh;
+    h_first = bh % nh;
     // Offsets clamped to [0, total]: a malformed list cannot index outside.
     const int start = min(max(p.cu[b], 0), p.T);
     T = min(max(p.cu[b + 1], start), p.T) - start;
-    head_row0 = (size_t)hd * p.T + start;
+    hrow_base = (size_t)start;
+    hrow_step = (size_t)p.T;
     tok_row0 = (size_t)start;
     if (ki * BKV >= T) return;  // past this sequence's end: uniform, before any barrier
   }
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, h = lane >> 5;
-  const int k0 = ki * BKV, kw0 = k0 + wave * KW;
-  const size_t head_off = head_row0 * N;
-  const bf16_bits* qg = p.q + head_off;
-  const bf16_bits* dg = p.dO + head_off;
+  const int h_end = TG ? p.H : h_first + 1;
+  for (int hd = h_first; hd < h_end; ++hd) {
+    const size_t head_row0 = hrow_base + (size_t)hd * hrow_step;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 31, h = lane >> 5;
+    const int k0 = ki * BKV, kw0 = k0 + wave * KW;
+    const size_t head_off = head_row0 * N;
+    const bf16_bits* qg = p.q + head_off;
+    const bf16_bits* dg = p.dO + head_off;
 
-  // K^T, V^T fragments (B operands): lane holds key kw0 + 32kb + c, d = 16ks + 8h.
-  bf16x8 kf[KB][KS];
-  u32x4* vw = vown + (size_t)wave * KS * 64;
+    // K^T, V^T fragments (B operands): lane holds key kw0 + 32kb + c, d = 16ks + 8h.
+    bf16x8 kf[KB][KS];
+    u32x4* vw = vown + (size_t)wave * KS * 64;
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    const size_t row = head_off + (size_t)min(kw0 + 32 * kb + c, T - 1) * N;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[kb][ks] = as_frag(ld16(p.k + row + 16 * ks + 8 * h));
-      vw[ks * 64 + lane] = ld16(p.v + row + 16 * ks + 8 * h);
-    }
-  }
-
-  float st_l = 0.f, st_d = 0.f;
-  if (tid < 2) stats[tid * (BQ + 1) + BQ] = u32x4{0u, 0u, 0u, 0u};
-  auto issue_tile = [&](int q0, int stage) {
-    bf16_bits* qt = tiles + stage * 2 * TILE;
-#pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int slot = (u * 4 + wave) * 64 + lane;
-      const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
-      const size_t off = (size_t)min(q0 + row, T - 1) * N + cc * 8;
-      g2lds16(qg + off, qt + (u * 4 + wave) * 512);
-      g2lds16(dg + off, qt + TILE + (u * 4 + wave) * 512);
-    }
-    if (tid < BQ) {
-      const size_t t = head_row0 + min(q0 + tid, T - 1);
-      st_l = p.lse[t];
-      st_d = p.delta[t];
-    }
-  };
-  // Called after wait_vmcnt0(): st_l / st_d are consumed only once every load
-  // of the tile has landed, so no wait is placed inside the prefetch.
-  auto publish_stats = [&](int stage) {
-    if (tid < BQ) stats[stage * (BQ + 1) + tid] = stat_pack(-st_l * kLog2e, -st_d);
-  };
-
-  f32x16 dv[KB][DB], dk[KB][DB];
-#pragma unroll
-  for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-    for (int db = 0; db < DB; ++db) dv[kb][db] = dk[kb][db] = zero16();
-
-  // Lane-constant parts of the fragment addresses (elements); a row's swizzle
-  // depends on row & 15 only.
-  const int g16 = lane >> 4, i16 = lane & 15;
-  const int tr_row = 4 * h + (i16 >> 2);
-  const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
-  // (Recomputed per use rather than held: registers are what bound the
-  // workgroups per CU.)
-  auto kofs = [&](int ks) { return swz_off<CH>(c, 16 * ks + 8 * h); };
-  auto tofs = [&](int x, int db) { return swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col); };
-  // Key-side selectors of the statistic k-block (the same in every lane: the
-  // query side is zero in the lanes holding k-elements 8..15).
-  const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
-
-  const int nq = (T - k0 + BQ - 1) / BQ;
-  issue_tile(k0, 0);
-  wait_vmcnt0();
-  publish_stats(0);
-  __syncthreads();
-  for (int it = 0; it < nq; ++it) {
-    const int q0 = k0 + it * BQ;
-    if (it + 1 < nq) issue_tile(q0 + BQ, (it + 1) & 1);
-    const bf16_bits* qt = tiles + (it & 1) * 2 * TILE;
-    const bf16_bits* dt = qt + TILE;
-    const u32x4* sts = stats + (it & 1) * (BQ + 1);
-    // One 32-query step in three parts: S and dP (MFMA), P and dS (exp2,
-    // multiply, convert; DIAG steps also mask key > query and query >= T),
-    // then the dV and dK updates (MFMA).
-    struct Sub {
-      f32x16 s, dp;
-      bf16x8 pb[2], sb[2];
-    };
-    auto sdp = [&](int sub, Sub& u) {
-      // Statistic k-block of the lane's query row qs0 + c (zero for h == 1).
-      const bf16x8 sa = as_frag(sts[h == 0 ? 32 * sub + c : BQ]);
-      u.s = mfma32(sa, sel_s, zero16());
-      u.dp = mfma32(sa, sel_d, zero16());
+    for (int kb = 0; kb < KB; ++kb) {
+      const size_t row = head_off + (size_t)min(kw0 + 32 * kb + c, T - 1) * N;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 qa = as_frag(*reinterpret_cast<const u32x4*>(qt + 32 * sub * N + kofs(ks)));
-        const bf16x8 da = as_frag(*reinterpret_cast<const u32x4*>(dt + 32 * sub * N + kofs(ks)));
-        u.s = mfma32(qa, kf[0][ks], u.s);
-        u.dp = mfma32(da, as_frag(vw[ks * 64 + lane]), u.dp);
+        kf[kb][ks] = as_frag(ld16(p.k + row + 16 * ks + 8 * h));
+        vw[ks * 64 + lane] = ld16(p.v + row + 16 * ks + 8 * h);
       }
-    };
-    auto soft = [&](int sub, Sub& u, auto diag_tag) {
-      constexpr bool DIAG = decltype(diag_tag)::value;
-      const int qs0 = q0 + 32 * sub, key = kw0 + c;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float pv = fast_exp2(u.s[i]);
-        if (DIAG) {
-          const int q = qs0 + 8 * (i >> 2) + 4 * h + (i & 3);
-          pv = (key > q || q >= T) ? 0.f : pv;
-        }
-        u.s[i] = pv;
-        u.dp[i] = pv * u.dp[i];
-      }
-#pragma unroll
-      for (int kst = 0; kst < 2; ++kst) {
-        u32x4 w, v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          w[e] = pack2(u.s[8 * kst + 2 * e], u.s[8 * kst + 2 * e + 1]);
-          v[e] = pack2(u.dp[8 * kst + 2 * e], u.dp[8 * kst + 2 * e + 1]);
-        }
-        u.pb[kst] = as_frag(w);
-        u.sb[kst] = as_frag(v);
-      }
-    };
-    auto kv = [&](int sub, const Sub& u) {
-#pragma unroll
-      for (int kst = 0; kst < 2; ++kst) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const int rb = (32 * sub + 16 * kst) * N;
-          const int o0 = rb + tofs(0, db), o1 = rb + tofs(1, db);
-          const bf16x8 dT = frag_from2(lds_read_tr4(dt + o0), lds_read_tr4(dt + o1));
-          const bf16x8 qT = frag_from2(lds_read_tr4(qt + o0), lds_read_tr4(qt + o1));
-          dv[0][db] = mfma32(dT, u.pb[kst], dv[0][db]);
-          dk[0][db] = mfma32(qT, u.sb[kst], dk[0][db]);
-        }
-      }
-    };
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int qs0 = q0 + 32 * sub;
-      if (qs0 + 31 < kw0 || qs0 >= T) continue;  // wave-uniform: nothing to add
-      Sub u;
-      sdp(sub, u);
-      if (qs0 < kw0 + KW - 1 || qs0 + 31 >= T)
-        soft(sub, u, std::true_type{});
-      else
-        soft(sub, u, std::false_type{});
-      kv(sub, u);
     }
-    wait_vmcnt0();
-    if (it + 1 < nq) publish_stats((it + 1) & 1);
-    __syncthreads();
-  }
 
-  // Epilogue per 32-key block: stage dV (then dK * scale) as fp32 rows and run
-  // the row-wise tails (rx scale; k RMSNorm + rotary backward for dK).
-  float* stg = reinterpret_cast<float*>(smem) + wave * 32 * FP;
+    float st_l = 0.f, st_d = 0.f;
+    if (tid < 2) stats[tid * (BQ + 1) + BQ] = u32x4{0u, 0u, 0u, 0u};
+    auto issue_tile = [&](int q0, int stage) {
+      bf16_bits* qt = tiles + stage * 2 * TILE;
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const f32x4 v = {dv[kb][db][4 * r4], dv[kb][db][4 * r4 + 1], dv[kb][db][4 * r4 + 2], dv[kb][db][4 * r4 + 3]};
-        *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v;
+      for (int u = 0; u < LOADS; ++u) {
+        const int slot = (u * 4 + wave) * 64 + lane;
+        const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+        const size_t off = (size_t)min(q0 + row, T - 1) * N + cc * 8;
+        g2lds16(qg + off, qt + (u * 4 + wave) * 512);
+        g2lds16(dg + off, qt + TILE + (u * 4 + wave) * 512);
       }
-    __syncthreads();
-    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, false, nullptr, 1.0f, nullptr, p.dav);
-    __syncthreads();
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const f32x4 v = {dk[kb][db][4 * r4], dk[kb][db][4 * r4 + 1], dk[kb][db][4 * r4 + 2], dk[kb][db][4 * r4 + 3]};
-        *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v * (p.scale / p.qscale);
+      if (tid < BQ) {
+        const size_t t = head_row0 + min(q0 + tid, T - 1);
+        st_l = p.lse[t];
+        st_d = p.delta[t];
       }
+    };
+    // Called after wait_vmcnt0(): st_l / st_d are consumed only once every load
+    // of the tile has landed, so no wait is placed inside the prefetch.
+    auto publish_stats = [&](int stage) {
+      if (tid < BQ) stats[stage * (BQ + 1) + tid] = stat_pack(-st_l * kLog2e, -st_d);
+    };
+
+    f32x16 dv[KB][DB], dk[KB][DB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) dv[kb][db] = dk[kb][db] = zero16();
+
+    // Lane-constant parts of the fragment addresses (elements); a row's swizzle
+    // depends on row & 15 only.
+    const int g16 = lane >> 4, i16 = lane & 15;
+    const int tr_row = 4 * h + (i16 >> 2);
+    const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+    // (Recomputed per use rather than held: registers are what bound the
+    // workgroups per CU.)
+    auto kofs = [&](int ks) { return swz_off<CH>(c, 16 * ks + 8 * h); };
+    auto tofs = [&](int x, int db) { return swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col); };
+    // Key-side selectors of the statistic k-block (the same in every lane: the
+    // query side is zero in the lanes holding k-elements 8..15).
+    const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
+
+    const int nq = (T - k0 + BQ - 1) / BQ;
+    issue_tile(k0, 0);
+    wait_vmcnt0();
+    publish_stats(0);
     __syncthreads();
-    head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, true, p.k, 1.0f, p.rk, p.dak);
-    __syncthreads();
+    for (int it = 0; it < nq; ++it) {
+      const int q0 = k0 + it * BQ;
+      if (it + 1 < nq) issue_tile(q0 + BQ, (it + 1) & 1);
+      const bf16_bits* qt = tiles + (it & 1) * 2 * TILE;
+      const bf16_bits* dt = qt + TILE;
+      const u32x4* sts = stats + (it & 1) * (BQ + 1);
+      // One 32-query step in three parts: S and dP (MFMA), P and dS (exp2,
+      // multiply, convert; DIAG steps also mask key > query and query >= T),
+      // then the dV and dK updates (MFMA).
+      struct Sub {
+        f32x16 s, dp;
+        bf16x8 pb[2], sb[2];
+      };
+      auto sdp = [&](int sub, Sub& u) {
+        // Statistic k-block of the lane's query row qs0 + c (zero for h == 1).
+        const bf16x8 sa = as_frag(sts[h == 0 ? 32 * sub + c : BQ]);
+        u.s = mfma32(sa, sel_s, zero16());
+        u.dp = mfma32(sa, sel_d, zero16());
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 qa = as_frag(*reinterpret_cast<const u32x4*>(qt + 32 * sub * N + kofs(ks)));
+          const bf16x8 da = as_frag(*reinterpret_cast<const u32x4*>(dt + 32 * sub * N + kofs(ks)));
+          u.s = mfma32(qa, kf[0][ks], u.s);
+          u.dp = mfma32(da, as_frag(vw[ks * 64 + lane]), u.dp);
+        }
+      };
+      auto soft = [&](int sub, Sub& u, auto diag_tag) {
+        constexpr bool DIAG = decltype(diag_tag)::value;
+        const int qs0 = q0 + 32 * sub, key = kw0 + c;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float pv = fast_exp2(u.s[i]);
+          if (DIAG) {
+            const int q = qs0 + 8 * (i >> 2) + 4 * h + (i & 3);
+            pv = (key > q || q >= T) ? 0.f : pv;
+          }
+          u.s[i] = pv;
+          u.dp[i] = pv * u.dp[i];
+        }
+#pragma unroll
+        for (int kst = 0; kst < 2; ++kst) {
+          u32x4 w, v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            w[e] = pack2(u.s[8 * kst + 2 * e], u.s[8 * kst + 2 * e + 1]);
+            v[e] = pack2(u.dp[8 * kst + 2 * e], u.dp[8 * kst + 2 * e + 1]);
+          }
+          u.pb[kst] = as_frag(w);
+          u.sb[kst] = as_frag(v);
+        }
+      };
+      auto kv = [&](int sub, const Sub& u) {
+#pragma unroll
+        for (int kst = 0; kst < 2; ++kst) {
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const int rb = (32 * sub + 16 * kst) * N;
+            const int o0 = rb + tofs(0, db), o1 = rb + tofs(1, db);
+            const bf16x8 dT = frag_from2(lds_read_tr4(dt + o0), lds_read_tr4(dt + o1));
+            const bf16x8 qT = frag_from2(lds_read_tr4(qt + o0), lds_read_tr4(qt + o1));
+            dv[0][db] = mfma32(dT, u.pb[kst], dv[0][db]);
+            dk[0][db] = mfma32(qT, u.sb[kst], dk[0][db]);
+          }
+        }
+      };
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int qs0 = q0 + 32 * sub;
+        if (qs0 + 31 < kw0 || qs0 >= T) continue;  // wave-uniform: nothing to add
+        Sub u;
+        sdp(sub, u);
+        if (qs0 < kw0 + KW - 1 || qs0 + 31 >= T)
+          soft(sub, u, std::true_type{});
+        else
+          soft(sub, u, std::false_type{});
+        kv(sub, u);
+      }
+      wait_vmcnt0();
+      if (it + 1 < nq) publish_stats((it + 1) & 1);
+      __syncthreads();
+    }
+
+    // Epilogue per 32-key block: stage dV (then dK * scale) as fp32 rows and run
+    // the row-wise tails (rx scale; k RMSNorm + rotary backward for dK).
+    float* stg = reinterpret_cast<float*>(smem) + wave * 32 * FP;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 v = {dv[kb][db][4 * r4], dv[kb][db][4 * r4 + 1], dv[kb][db][4 * r4 + 2], dv[kb][db][4 * r4 + 3]};
+          *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v;
+        }
+      __syncthreads();
+      head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, false, nullptr, 1.0f, nullptr, p.dav);
+      __syncthreads();
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 v = {dk[kb][db][4 * r4], dk[kb][db][4 * r4 + 1], dk[kb][db][4 * r4 + 2], dk[kb][db][4 * r4 + 3]};
+          *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v * (p.scale / p.qscale);
+        }
+      __syncthreads();
+      head_row_bwd<N, TG>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, true, p.k, 1.0f, p.rk, p.dak, false);
+      __syncthreads();
+    }
   }
 }
 
-hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
+template <int N, bool VAR, bool TG>
+struct DqKernel {
+  static void launch(const AttnBwdParams& p, int G, hipStream_t s) {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<N, VAR, TG>), dim3(G), dim3(256), 0, s, p);
+  }
+};
+template <int N, bool VAR, bool TG>
+struct DkdvKernel {
+  static void launch(const AttnBwdParams& p, int G, hipStream_t s) {
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<N, VAR, TG>), dim3(G), dim3(256), 0, s, p);
+  }
+};
+
+template <template <int, bool, bool> class K>
+static hipError_t launch_bwd_variant(const AttnBwdParams& p, int N, int blocks_per_seq, hipStream_t s) {
   if (p.sl2e != 1.0f) return hipErrorInvalidValue;  // stored q must be in log2 units
-  const int BQ = 128;
-  const bool var = p.cu != nullptr;
-  const int G = var ? p.nseq * p.H * ((p.max_len + BQ - 1) / BQ) : p.B * p.H * ((p.T + BQ - 1) / BQ);
-  if (N == 64 && !var)
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
-  else if (N == 64)
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
-  else if (!var)
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
+  const bool var = p.cu != nullptr, tg = p.tpart != nullptr;
+  // Grid: (sequence, head, block); with table partials a workgroup walks
+  // every head of its (sequence, block).
+  const int G = (var ? p.nseq : p.B) * (tg ? 1 : p.H) * blocks_per_seq;
+  if (G <= 0) return hipSuccess;
+  const int v = (N == 128 ? 4 : 0) | (var ? 2 : 0) | (tg ? 1 : 0);
+  switch (v) {
+    case 0: K<64, false, false>::launch(p, G, s); break;
+    case 1: K<64, false, true>::launch(p, G, s); break;
+    case 2: K<64, true, false>::launch(p, G, s); break;
+    case 3: K<64, true, true>::launch(p, G, s); break;
+    case 4: K<128, false, false>::launch(p, G, s); break;
+    case 5: K<128, false, true>::launch(p, G, s); break;
+    case 6: K<128, true, false>::launch(p, G, s); break;
+    default: K<128, true, true>::launch(p, G, s); break;
+  }
   return hipGetLastError();
 }
 
+hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s) {
+  const int BQ = 128, len = p.cu != nullptr ? p.max_len : p.T;
+  return launch_bwd_variant<DqKernel>(p, N, (len + BQ - 1) / BQ, s);
+}
+
 hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s) {
-  if (p.sl2e != 1.0f) return hipErrorInvalidValue;  // stored q must be in log2 units
-  const int BKV = 128;
-  const bool var = p.cu != nullptr;
-  const int G = var ? p.nseq * p.H * ((p.max_len + BKV - 1) / BKV) : p.B * p.H * ((p.T + BKV - 1) / BKV);
-  if (N == 64 && !var)
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
-  else if (N == 64)
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
-  else if (!var)
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
+  const int BKV = 128, len = p.cu != nullptr ? p.max_len : p.T;
+  return launch_bwd_variant<DkdvKernel>(p, N, (len + BKV - 1) / BKV, s);
+}
+
+// dF1 / dF2 from the per-token partials: one thread per 4 columns of one
+// position t, summing the rows of position t of every sequence that reaches
+// it, sequence after sequence (a fixed order: the result is deterministic).
+__global__ __launch_bounds__(256) void table_grad_reduce_kernel(const float* tpart, const int* cu, int nseq,
+                                                                int B, int T, int N, int rows, float* df1,
+                                                                float* df2) {
+  const int q = N / 2;  // 4-column groups per position (2N columns)
+  const int id = blockIdx.x * 256 + threadIdx.x;
+  if (id >= rows * q) return;
+  const int t = id / q, j = (id - t * q) * 4;
+  f32x4 acc = zero4();
+  if (cu == nullptr) {
+    for (int b = 0; b < B; ++b) acc += *reinterpret_cast<const f32x4*>(tpart + ((size_t)b * T + t) * (2 * N) + j);
+  } else {
+    for (int sq = 0; sq < nseq; ++sq) {
+      const int start = min(max(cu[sq], 0), T);
+      const int len = min(max(cu[sq + 1], start), T) - start;
+      if (t < len) acc += *reinterpret_cast<const f32x4*>(tpart + ((size_t)start + t) * (2 * N) + j);
+    }
+  }
+  float* dst = j < N ? df1 + (size_t)t * N + j : df2 + (size_t)t * N + (j - N);
+  *reinterpret_cast<f32x4*>(dst) = acc;
+}
+
+hipError_t launch_table_grad_reduce(const AttnBwdParams& p, int N, int rows, float* df1, float* df2,
+                                    hipStream_t s) {
+  const int n = rows * (N / 2);
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(table_grad_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p.tpart, p.cu, p.nseq, p.B,
+                     p.T, N, rows, df1, df2);
   return hipGetLastError();
 }
 

@@ -87,7 +87,7 @@ def bwd_grads(x, wq, wk, wv, wg, wo, factor1, factor2, o_save, lse, dy, H, N, ep
     df1 = torch.empty((T, N), device=dev, dtype=torch.float32) if table_grad else None
     df2 = torch.empty((T, N), device=dev, dtype=torch.float32) if table_grad else None
     d = _d(x.shape, H, N, eps)
-    ws_bytes = lib.mea_workspace_bytes(d, _lib.MEA_PASS_BWD)
+    ws_bytes = lib.mea_workspace_bytes(d, _lib.MEA_PASS_BWD_TABLES if table_grad else _lib.MEA_PASS_BWD)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     ws_w = [w.contiguous() for w in (wq, wk, wv, wg, wo)]
     with torch.cuda.device(dev):

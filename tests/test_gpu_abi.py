@@ -63,7 +63,7 @@ def test_guarded_forward_backward(w):
     dwbufs = [_guarded(HN * C, torch.bfloat16) for _ in range(4)] + [_guarded(C * HN, torch.bfloat16)]
     df1b, df1 = _guarded(T * N, torch.float32)
     df2b, df2 = _guarded(T * N, torch.float32)
-    wsb = lib.mea_workspace_bytes(ctypes.byref(d), 1)
+    wsb = lib.mea_workspace_bytes(ctypes.byref(d), _lib.MEA_PASS_BWD_TABLES)  # df1 / df2 are written
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     rc = lib.mea_bwd(ctypes.byref(d), g["dy"].data_ptr(), g["x"].data_ptr(),
                      *(g[n].data_ptr() for n in ("wq", "wk", "wv", "wg", "wo")), f1.data_ptr(), f2.data_ptr(),

@@ -150,11 +150,15 @@ def test_zero_gate_known_answer():
     assert torch.all(sig == 0.5)
 
 
-def test_deterministic():
+@pytest.mark.parametrize("table_grad", [False, True], ids=["buffers", "trainable-tables"])
+def test_deterministic(table_grad):
+    """Two runs are bitwise equal, table gradients included (their sum over
+    batch and heads runs in a fixed order)."""
     inp = make_inputs(W0)
-    a = gpu_block(inp, W0.H, W0.N, table_grad=False)
-    b = gpu_block(inp, W0.H, W0.N, table_grad=False)
-    for k in ("y", "dx", "dwq", "dwk", "dwv", "dwg", "dwo"):
+    a = gpu_block(inp, W0.H, W0.N, table_grad=table_grad)
+    b = gpu_block(inp, W0.H, W0.N, table_grad=table_grad)
+    keys = ("y", "dx", "dwq", "dwk", "dwv", "dwg", "dwo") + (("df1", "df2") if table_grad else ())
+    for k in keys:
         assert torch.equal(a[k], b[k]), k
 
 

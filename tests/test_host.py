@@ -63,6 +63,9 @@ def test_workspace_bytes(lib):
     M, HN = 2 * 256, 4 * 64
     assert fwd >= 5 * M * HN * 2
     assert bwd > fwd
+    # Table gradients need per-token partials: B * T * 2N fp32 more.
+    tab = lib.mea_workspace_bytes(ctypes.byref(_d()), _lib.MEA_PASS_BWD_TABLES)
+    assert tab - bwd >= M * 2 * 64 * 4
     # Invalid descriptors report 0.
     for bad in (_d(N=96), _d(C=300), _d(T_max=10), _d(eps=0.0), _d(B=0)):
         assert lib.mea_workspace_bytes(ctypes.byref(bad), 0) == 0
@@ -115,6 +118,9 @@ def test_pointer_and_workspace_validation(lib):
     b_one_df[18] = None
     assert lib.mea_bwd(ctypes.byref(d), *b_one_df, 10, None) == _header_enum("MEA_ERR_NULL")
     assert lib.mea_bwd(ctypes.byref(d), *bargs, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
+    # The backward-only workspace is too small once table gradients are asked for.
+    wsb = lib.mea_workspace_bytes(ctypes.byref(d), _lib.MEA_PASS_BWD)
+    assert lib.mea_bwd(ctypes.byref(d), *bargs, wsb, None) == _header_enum("MEA_ERR_WORKSPACE")
     # dx overlapping another argument (it holds a transient before the
     # result): refused before the workspace is even looked at.
     for other in (0, 1, 9, 19):
