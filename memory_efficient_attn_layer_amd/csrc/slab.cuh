@@ -2,10 +2,12 @@
 //
 // A slab holds R operand rows x KS bf16 of the reduction dimension k, KS = 64
 // (8 chunks of 16 bytes per row) or 32 (4 chunks). Chunk c of row r sits at
-// chunk slot c ^ slab_swz<KS>(r): with 64-element rows two rows fill one
-// 256-byte LDS bank line (swizzle (r >> 1) & 7), with 32-element rows four do
-// (swizzle (r >> 2) & 3); either way the 16 rows that one 16-lane group reads
-// at one chunk index land in 16 distinct 16-byte bank groups.
+// chunk slot c ^ slab_swz<KS>(r). The MFMA operand read has lane 16g + i
+// fetch chunk g of row r0 + i. For 32-element rows the slot of row r is
+// (r >> 1) & 3: measured on gfx950 (ds_read_b128 in this pattern, rocprofv3
+// SQ_LDS_BANK_CONFLICT), it is conflict-free and reads 223 B/clk per CU,
+// where (r >> 2) & 3, r & 3 or no swizzle conflict on half the cycles
+// (132 B/clk). 64-element rows use (r >> 1) & 7.
 //
 // Slabs are filled straight from global memory with global_load_lds_dwordx4:
 // one wave instruction writes 1 KB of LDS (64 / CH rows), lane L filling slot
@@ -22,7 +24,7 @@ constexpr int kSlabK = 64;  // k elements per row of a 64-wide slab
 template <int KS>
 __device__ __forceinline__ int slab_swz(int row) {
   static_assert(KS == 64 || KS == 32, "slab width");
-  return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+  return KS == 64 ? ((row >> 1) & 7) : ((row >> 1) & 3);
 }
 
 // Issues the loads of an R-row slab into LDS byte address lds, shared by the
