@@ -59,10 +59,12 @@ def kernel_work(w):
         "qkvg_proj": dict(flops=2.0 * M * C * 4 * HN, bytes=2.0 * M * C + 2.0 * 4 * M * HN),
         "attn_fwd": dict(flops=2 * pair, bytes=2.0 * 4 * M * HN),
         "gate_oproj": dict(flops=2.0 * M * HN * C, bytes=2.0 * 2 * M * HN + 2.0 * M * C),
-        "dz_gate_bwd": dict(flops=2.0 * M * C * HN, bytes=2.0 * M * C + 2.0 * 4 * M * HN),
+        # reads dy, O, sigmoid(a_g); writes dO, da_g and z = O * sigmoid(a_g)
+        "dz_gate_bwd": dict(flops=2.0 * M * C * HN, bytes=2.0 * M * C + 2.0 * 5 * M * HN),
         "attn_bwd_dq": dict(flops=1 * pair, bytes=2.0 * 5 * M * HN),
         "attn_bwd_dkdv": dict(flops=3 * pair, bytes=2.0 * 6 * M * HN),
-        "dw_partial": dict(flops=2.0 * M * (4 * HN * C + C * HN), bytes=2.0 * M * (4 * HN + C + C + 2 * HN)),
+        # reads da (4 parts), x, dy and z
+        "dw_partial": dict(flops=2.0 * M * (4 * HN * C + C * HN), bytes=2.0 * M * (4 * HN + C + C + HN)),
         "dx": dict(flops=2.0 * M * 4 * HN * C, bytes=2.0 * M * (4 * HN + 2 * C)),
     }
 
