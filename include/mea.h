@@ -30,8 +30,8 @@
  *   - Tensors are dense row-major in the shapes documented per argument.
  *     Pointers must be 16-byte aligned.
  *
- * Supported shapes: N in {64, 128}; C a multiple of 256 with C <= 1024 for
- * the backward pass (C <= 4096 forward); H >= 1; B, T >= 1; T <= T_max; and
+ * Supported shapes: N in {64, 128}; C a multiple of 256, C <= 4096; H >= 1;
+ * B, T >= 1; T <= T_max; and
  * for the backward H * (T + 256) * N < 2^30 (one batch's head-major gradient
  * rows are addressed with 32-bit byte offsets).
  */
@@ -129,7 +129,9 @@ int mea_fwd(const mea_desc* d, const void* x, const void* wq, const void* wk,
  *
  * dx also holds the gradient of the gate projection's output (rows of H*N
  * values at stride C) until the last kernel overwrites it with the result,
- * when H*N <= C; it must not overlap any other argument (MEA_ERR_ALIAS).
+ * when H*N <= C <= 1024, and partial results of the last kernel's feature
+ * groups when C > 1024; it must not overlap any other argument
+ * (MEA_ERR_ALIAS).
  */
 int mea_bwd(const mea_desc* d, const void* dy, const void* x, const void* wq,
             const void* wk, const void* wv, const void* wg, const void* wo,

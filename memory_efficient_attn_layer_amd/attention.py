@@ -29,7 +29,7 @@ from . import _lib
 
 SUPPORTED_HEAD_DIMS = (64, 128)
 MAX_C_FORWARD = 4096
-MAX_C_BACKWARD = 1024
+MAX_C_BACKWARD = 4096
 
 
 def _validate(x, weights, factor1, factor2, H: int, N: int, eps: float, need_backward: bool) -> None:

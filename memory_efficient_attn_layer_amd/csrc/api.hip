@@ -43,8 +43,10 @@ Layout make_layout(const mea_desc& d, int pass) {
   } else {
     L.dO = take(act);
     L.daq = take(act);
-    // da_g lives in the caller's dx buffer when its rows fit (HN <= C).
-    L.dag = HN <= C ? 0 : take(act);
+    // da_g lives in the caller's dx buffer when its rows fit (HN <= C) and
+    // dx is written once, at the end (C <= 1024; wider rows take dx as
+    // scratch for their feature groups).
+    L.dag = HN <= C && C <= 1024 ? 0 : take(act);
     L.rx = take(M * 4);
     L.rq = take(stat);
     L.rk = take(stat);
@@ -64,8 +66,7 @@ int validate(const mea_desc* d, int pass) {
   if (d->N != 64 && d->N != 128) return MEA_ERR_HEAD_DIM;
   if (d->C < 256 || d->C % 256 != 0) return MEA_ERR_MODEL_DIM;
   const bool bwd = pass == MEA_PASS_BWD || pass == MEA_PASS_BWD_TABLES;
-  if (bwd && d->C > 1024) return MEA_ERR_MODEL_DIM;
-  if (pass == MEA_PASS_FWD && d->C > 4096) return MEA_ERR_MODEL_DIM;
+  if (d->C > 4096) return MEA_ERR_MODEL_DIM;
   if (!(d->eps > 0.f) || !isfinite(d->eps)) return MEA_ERR_EPS;
   // All row and element indices used by the kernels fit in 31 bits.
   const int64_t M = d->B * d->T, HN = d->H * d->N;
@@ -506,7 +507,7 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
   // da_g token-major, in the rows of dx when they are wide enough (each dx
   // workgroup reads the da_g rows it later overwrites, and nothing else
   // reads them after the weight gradients).
-  const bool dag_in_dx = HN <= C;
+  const bool dag_in_dx = HN <= C && C <= 1024;
   const BwdBufs bf = bwd_bufs(d, ws, dag_in_dx ? dx : nullptr, C);
   rc = bwd_front(d, var, dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, df1, df2, bf, ws, stream);
   if (rc != MEA_OK) return rc;
@@ -830,7 +831,7 @@ const char* mea_strerror(int code) {
     case MEA_ERR_NULL: return "a required pointer is NULL (or only one of a pair was given)";
     case MEA_ERR_SHAPE: return "B, T, H must be >= 1, T <= T_max, and indices must fit 31 bits";
     case MEA_ERR_HEAD_DIM: return "head width N must be 64 or 128";
-    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 256 (<= 1024 backward, <= 4096 forward)";
+    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 256 and <= 4096";
     case MEA_ERR_WORKSPACE: return "workspace smaller than mea_workspace_bytes()";
     case MEA_ERR_ALIGN: return "a pointer is not 16-byte aligned";
     case MEA_ERR_EPS: return "eps must be finite and positive";

@@ -359,6 +359,200 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
   }
 }
 
+// ---------------------------------------------------------------------------
+// dx for C > 1024 (a multiple of 256): the workgroup layout of dx_kernel<1024>
+// (8 waves of 128 features x 64 tokens) walks the output features in groups
+// of 1024. The RMSNorm-backward dot (acc . x) needs the whole row, so it is
+// summed over the groups in LDS; every group but the last leaves its
+// uncorrected acc (bf16) in dx, the last group writes its result directly,
+// and then every thread re-reads exactly the 16-byte chunks it wrote for the
+// earlier groups, applies the correction and writes them back (a thread's
+// own store is visible to its own later load once vmcnt has drained; no
+// other workgroup touches these rows, and da_g does not live in dx here).
+// Weight rows past C are clamped on load; a wave's 128-feature slice is then
+// either wholly inside C or wholly past it (C and the groups are multiples
+// of 128) and the latter stores nothing.
+// ---------------------------------------------------------------------------
+constexpr int kDxGroup = 1024;
+
+__global__ __launch_bounds__(512, 1) void dx_wide_kernel(DxParams p) {
+  constexpr int CG = kDxGroup, WF = 8, NW = 8, BT = 64, BK = 32, NS = 2;
+  constexpr int STAGE = (CG + BT) * BK;
+  constexpr int FB = 8, TB = 4;
+  constexpr int SP = 128 + 8;  // staging pitch (elements)
+  __shared__ __attribute__((aligned(16))) bf16_bits smem[NS * STAGE];
+  __shared__ float dotp[WF][BT];
+  __shared__ float dsum[BT];
+
+  const int M = p.M, C = p.C, K4 = 4 * p.HN;
+  const int m0 = xcd_remap(blockIdx.x, (M + BT - 1) / BT) * BT;
+  const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wf = wave;  // one token block of 64: waves run along features only
+  const bf16_bits* wt_g = p.wcatT;  // (C, 4HN)
+  const DaParts& dp = p.da;
+  const int N = dp.N, T = dp.T;
+  const int ngroups = (C + CG - 1) / CG;
+  if (tid < BT) dsum[tid] = 0.f;
+
+  using Plan = SlabPlan<BT, NW, BK>;
+  auto mf = [&](int u) { return min(m0 + u * NW * 16, M - 1); };
+  auto hm = [&](int m) { return (m / T) * (dp.H - 1) * T + m; };
+  Plan plan_t, plan_h;
+  slab_plan(plan_t, wave, dp.ld_g, [&](int u, int i) { return min(m0 + u * NW * 16 + i, M - 1) - mf(u); });
+  slab_plan(plan_h, wave, N, [&](int u, int i) { return hm(min(m0 + u * NW * 16 + i, M - 1)) - hm(mf(u)); });
+  int hmf[Plan::NU];
+#pragma unroll
+  for (int u = 0; u < Plan::NU; ++u) hmf[u] = __builtin_amdgcn_readfirstlane(hm(mf(u)));
+  const uint32_t lds0 = lds_addr(smem);
+  const bf16_bits* xg = p.x;
+  const float inv_c = 1.0f / (float)C;
+  int mrow[TB];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) mrow[tb] = min(m0 + tb * 16 + c16, M - 1);
+
+  for (int grp = 0; grp < ngroups; ++grp) {
+    const int f0 = grp * CG;
+    const bool wave_live = f0 + wf * 128 < C;  // wave-uniform
+    const bool last = grp == ngroups - 1;
+    int part = 0, hh = 0, n0 = 0;
+    auto issue = [&](int ks, int st) {
+      const uint32_t lds = lds0 + (uint32_t)(st * STAGE) * 2u;
+      const int k0 = ks * BK;
+      // Weight rows f0 .. f0 + CG - 1, clamped to C - 1 (a clamped base keeps
+      // every row offset non-negative).
+      slab_issue<CG, NW, BK>(
+          lds, wave, K4, [&](int u) { return wt_g + (size_t)min(f0 + u * NW * 16, C - 1) * K4 + k0; },
+          [&](int u, int i) { return min(f0 + u * NW * 16 + i, C - 1) - min(f0 + u * NW * 16, C - 1); });
+      {
+        const bool tokm = part == 3;
+        const bf16_bits* src = da_part(dp, part);
+        constexpr int NU = Plan::NU, NI = Plan::NI;
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+          const int ins = u * NW + wave;
+          if (NI % NW != 0 && ins >= NI) break;  // wave-uniform: partial last round
+          const size_t off = tokm ? (size_t)mf(u) * dp.ld_g + (hh * N + n0) : ((size_t)hh * T + hmf[u]) * N + n0;
+          g2lds16_s(src + off, tokm ? plan_t.voff[u] : plan_h.voff[u],
+                    lds + (uint32_t)(CG * BK * 2) + (uint32_t)ins * 1024u);
+        }
+      }
+      n0 += BK;
+      if (n0 == N) {
+        n0 = 0;
+        if (++hh == dp.H) {
+          hh = 0;
+          ++part;
+        }
+      }
+    };
+
+    f32x4 acc[FB][TB];
+#pragma unroll
+    for (int fb = 0; fb < FB; ++fb)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = zero4();
+
+    const int nk = K4 / BK;
+    issue(0, 0);
+    for (int ks = 0; ks < nk; ++ks) {
+      wait_vmcnt0();
+      __syncthreads();
+      if (ks + 1 < nk) issue(ks + 1, (ks + 1) % NS);
+      const bf16_bits* As = smem + (ks % NS) * STAGE;
+      const bf16_bits* Bs = As + CG * BK;
+      bf16x8 af[FB], bfr[TB];
+#pragma unroll
+      for (int fb = 0; fb < FB; ++fb) af[fb] = as_frag(slab_read<BK>(As, wf * 128 + fb * 16 + c16, g));
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) bfr[tb] = as_frag(slab_read<BK>(Bs, tb * 16 + c16, g));
+#pragma unroll
+      for (int fb = 0; fb < FB; ++fb)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = mfma(af[fb], bfr[tb], acc[fb][tb]);
+    }
+
+    // acc . x over this wave's 128 features, summed over the waves and the
+    // groups in dsum.
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      float d = 0.f;
+      if (wave_live) {
+#pragma unroll
+        for (int fb = 0; fb < FB; ++fb) {
+          const u32x2 xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + f0 + wf * 128 + 16 * fb + 4 * g);
+          d += acc[fb][tb][0] * lo_bf(xv[0]) + acc[fb][tb][1] * hi_bf(xv[0]) + acc[fb][tb][2] * lo_bf(xv[1]) +
+               acc[fb][tb][3] * hi_bf(xv[1]);
+        }
+      }
+      d += shfl_xor(d, 16);
+      d += shfl_xor(d, 32);
+      if (g == 0) dotp[wf][tb * 16 + c16] = d;
+    }
+    __syncthreads();  // also: every wave is past its last slab read
+    if (tid < BT) {
+      float t = dsum[tid];
+#pragma unroll
+      for (int i = 0; i < WF; ++i) t += dotp[i][tid];
+      dsum[tid] = t;
+    }
+    __syncthreads();
+
+    // The last group writes dx = acc - x rx^2 (acc . x) / C; the others write
+    // acc. Staged per 16-token block and stored as whole 256-byte segments.
+    bf16_bits* stg = smem + wave * 16 * SP;
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int tl = tb * 16 + c16;
+      const float rxv = p.rx[mrow[tb]];
+      const float cf = last ? rxv * rxv * dsum[tl] * inv_c : 0.f;
+#pragma unroll
+      for (int fb = 0; fb < FB; ++fb) {
+        u32x2 xv = {0u, 0u};
+        if (last && wave_live)
+          xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + f0 + wf * 128 + 16 * fb + 4 * g);
+        const f32x4& a = acc[fb][tb];
+        const float o0 = a[0] - lo_bf(xv[0]) * cf, o1 = a[1] - hi_bf(xv[0]) * cf;
+        const float o2 = a[2] - lo_bf(xv[1]) * cf, o3 = a[3] - hi_bf(xv[1]) * cf;
+        *reinterpret_cast<u32x2*>(stg + c16 * SP + 16 * fb + 4 * g) = u32x2{pack2(o0, o1), pack2(o2, o3)};
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+#pragma unroll
+      for (int it = 0; it < 16 * 16 / 64; ++it) {
+        const int id = lane + 64 * it, row = id >> 4, ch = id & 15;
+        const int m = m0 + tb * 16 + row;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * SP + ch * 8);
+        if (m < M && wave_live) st16(p.dx + (size_t)m * C + f0 + wf * 128 + ch * 8, val);
+      }
+    }
+    __syncthreads();  // the staging area is the next group's slab ring
+  }
+
+  // Correct the earlier groups: each thread reloads the chunks it stored.
+  wait_vmcnt0();
+  for (int grp = 0; grp + 1 < ngroups; ++grp) {
+    const int f0 = grp * CG;
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+      for (int it = 0; it < 16 * 16 / 64; ++it) {
+        const int id = lane + 64 * it, row = id >> 4, ch = id & 15;
+        const int m = m0 + tb * 16 + row;
+        if (m >= M || f0 + wf * 128 >= C) continue;
+        const size_t off = (size_t)m * C + f0 + wf * 128 + ch * 8;
+        const float rxv = p.rx[m];
+        const float cf = rxv * rxv * dsum[tb * 16 + row] * inv_c;
+        float a[8], xv[8], o[8];
+        unpack8(ld16(p.dx + off), a);
+        unpack8(ld16(xg + off), xv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = a[e] - xv[e] * cf;
+        st16(p.dx + off, pack8(o));
+      }
+    }
+  }
+}
+
 hipError_t launch_dx(const DxParams& p, hipStream_t s) {
   switch (p.C) {
     case 256:
@@ -374,7 +568,8 @@ hipError_t launch_dx(const DxParams& p, hipStream_t s) {
       hipLaunchKernelGGL(dx_kernel<1024>, dim3((p.M + 63) / 64), dim3(512), 0, s, p);
       break;
     default:
-      return hipErrorInvalidValue;
+      if (p.C <= 1024 || p.C % 256 != 0) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(dx_wide_kernel, dim3((p.M + 63) / 64), dim3(512), 0, s, p);
   }
   return hipGetLastError();
 }

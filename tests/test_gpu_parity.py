@@ -102,6 +102,11 @@ BLOCK_CASES = [
     # H*N not a multiple of 256: the dZ kernel's last feature group is partial.
     ("h5-hn320-b1-t150", _w("h5", 1, 150, 256, 5, 64), None),
     ("h3-hn192-b2-t70", _w("h3", 2, 70, 512, 3, 64), None),
+    # C > 1024: dx walks the features in groups of 1024 (the last one partial
+    # for C = 1280); the prefill widths (C = H*N = 2048, N = 128, YaRN s = 8).
+    ("c1280-h5-b2-t100", _w("c1280", 2, 100, 1280, 5, 64), None),
+    ("c2048-h16-n128-yarn8-b1-t256", _w("c2048", 1, 256, 2048, 16, 128, 8.0, 64), None),
+    ("c3072-h4-b1-t64", _w("c3072", 1, 64, 3072, 4, 64), None),
 ]
 
 

@@ -127,9 +127,10 @@ def test_pointer_and_workspace_validation(lib):
         b_alias = list(bargs)
         b_alias[11] = bargs[other] + (4096 if other != 19 else 0)  # the workspace is 10 bytes here
         assert lib.mea_bwd(ctypes.byref(d), *b_alias, 10, None) == _header_enum("MEA_ERR_ALIAS")
-    # C > 1024 is forward-only.
-    d2 = _d(C=2048)
+    # C above 4096 is refused in both passes.
+    d2 = _d(C=4352)
     assert lib.mea_bwd(ctypes.byref(d2), *bargs, 1 << 40, None) == _header_enum("MEA_ERR_MODEL_DIM")
+    assert lib.mea_workspace_bytes(ctypes.byref(_d(C=2048, H=16, N=128)), _lib.MEA_PASS_BWD) > 0
 
 
 def test_decode_and_prefill_validation(lib):
@@ -185,7 +186,7 @@ def test_varlen_validation(lib):
     # bwd: dy x wq wk wv wg wo f1 f2 o lse dx dwq dwk dwv dwg dwo df1 df2 ws
     bargs = [(1 << 32) + i * (1 << 28) for i in range(20)]
     assert lib.mea_bwd_varlen(ctypes.byref(d), fake, 4, 300, *bargs, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
-    assert lib.mea_bwd_varlen(ctypes.byref(_d(B=1, T=1000, T_max=300, C=2048)), fake, 4, 300, *bargs, 1 << 40,
+    assert lib.mea_bwd_varlen(ctypes.byref(_d(B=1, T=1000, T_max=300, C=4352)), fake, 4, 300, *bargs, 1 << 40,
                               None) == _header_enum("MEA_ERR_MODEL_DIM")
 
 
@@ -230,25 +231,39 @@ def test_module_and_tables_construct_on_cpu():
         fused_attn(x, m.q_proj, m.k_proj, m.v_proj, m.g_proj, m.o_proj, y, 4, 64)
 
 
-def test_save_decision_follows_grad_mode():
-    """Whether the forward saves activations (and so needs the backward's
-    width limit, C <= 1024) is decided from grad mode and requires_grad
-    before Function.forward runs: under no_grad / inference_mode a module
-    with C = 2048 gets past validation to the device check (no GPU here),
-    while with grad enabled it is refused for its width."""
-    m = CausalSoftmaxAttention(2048, 16, 128).bfloat16()
-    y = Yarn(128, 16)
-    x = torch.randn(1, 16, 2048, dtype=torch.bfloat16)
+def test_save_decision_follows_grad_mode(monkeypatch):
+    """Whether the forward saves activations is decided from grad mode and
+    requires_grad before Function.forward runs (inside it grad mode is always
+    off, and ctx.needs_input_grad reports True for a Parameter even under
+    no_grad): no_grad / inference_mode and parameters that need no grad all
+    give need_backward=False."""
+    import memory_efficient_attn_layer_amd.attention as att
+
+    seen = []
+
+    def record(x, weights, f1, f2, H, N, eps, need_backward):
+        seen.append(need_backward)
+        raise RuntimeError("validation reached")
+
+    monkeypatch.setattr(att, "_validate", record)
+    m = CausalSoftmaxAttention(256, 4, 64).bfloat16()
+    y = Yarn(64, 16)
+    x = torch.randn(1, 16, 256, dtype=torch.bfloat16)
     for ctx in (torch.no_grad, torch.inference_mode):
-        with ctx(), pytest.raises(RuntimeError, match="ROCm GPU"):
+        with ctx(), pytest.raises(RuntimeError, match="validation reached"):
             m(x, y)
-    with pytest.raises(ValueError, match="backward supports"):
+        assert seen[-1] is False
+    with pytest.raises(RuntimeError, match="validation reached"):
         m(x, y)
-    # Nothing requires grad: no save even with grad mode on.
+    assert seen[-1] is True
     for p in m.parameters():
         p.requires_grad_(False)
-    with pytest.raises(RuntimeError, match="ROCm GPU"):
+    with pytest.raises(RuntimeError, match="validation reached"):
         m(x, y)
+    assert seen[-1] is False
+    with pytest.raises(RuntimeError, match="validation reached"):
+        m(x.requires_grad_(True), y)  # an input that needs grad is enough
+    assert seen[-1] is True
 
 
 def test_static_decode_validation(lib):
