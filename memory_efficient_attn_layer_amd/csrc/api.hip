@@ -396,11 +396,11 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
 
   // Weight transposes (k-contiguous B operands for dZ and dx).
   MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_transpose(static_cast<const bf16_bits*>(wo), C, HN, HN, bf.woT, C, 0, s); }));
-  const void* wp[4] = {wq, wk, wv, wg};
-  for (int j = 0; j < 4; ++j)
-    MEA_TRY(timed(K_TRANSPOSE, s, [&] {
-      return mea::launch_transpose(static_cast<const bf16_bits*>(wp[j]), HN, C, C, bf.wcatT, 4 * HN, j * HN, s);
-    }));
+  {
+    mea::WcatPackParams wp{static_cast<const bf16_bits*>(wq), static_cast<const bf16_bits*>(wk),
+                           static_cast<const bf16_bits*>(wv), static_cast<const bf16_bits*>(wg), bf.wcatT, HN, C};
+    MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_wcat_pack(wp, s); }));
+  }
   // Recompute q, k, v, sigmoid(g) and the three RMS statistics.
   const float qs = q_log2_scale(N);
   int* tpos = nullptr;

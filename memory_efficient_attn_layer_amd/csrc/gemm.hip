@@ -197,7 +197,8 @@ __device__ __forceinline__ const bf16_bits* da_part(const DaParts& dp, int part)
 // dx = rmsnorm_bwd([da_q|da_k|da_v|da_g] Wcat), one workgroup owns full rows.
 //
 // Computed transposed, D^T = Wcat^T da^T: A = Wcat^T rows (C features, k =
-// 4HN contiguous), B = da rows (tokens). A 32-wide k-slab of da lies in one
+// 4HN, stored k-slab-major by wcat_pack_kernel so that a slab is one
+// contiguous block), B = da rows (tokens). A 32-wide k-slab of da lies in one
 // head of one part (N >= 64): each slab has one base address, and a lane's
 // row offset from it, the same in every slab, is precomputed for the
 // head-major parts (q, k, v) and for the token-major da_g. A workgroup
@@ -221,8 +222,9 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
   // Load instructions every wave issues per slab at least (waves whose
   // share is larger wait for more of their own loads, which is still right).
   constexpr int LOADS = (C / 16) / NW + (BT / 16) / NW;
-  constexpr int SP = 128 + 8;                           // staging pitch (elements)
-  __shared__ __attribute__((aligned(16))) bf16_bits smem[NS * STAGE];
+  constexpr int XW = 64 * 128;                          // x block of one wave (elements)
+  constexpr int SMEM = NS * STAGE > NW * XW ? NS * STAGE : NW * XW;
+  __shared__ __attribute__((aligned(16))) bf16_bits smem[SMEM];
   __shared__ float dotp[WF][BT];
 
   const int M = p.M, K4 = 4 * p.HN;
@@ -230,7 +232,7 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
   const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wf = wave % WF, wt = wave / WF;
-  const bf16_bits* wt_g = p.wcatT;  // (C, 4HN)
+  const bf16_bits* wt_g = p.wcatT;  // (4HN / 32, C, 32): k-slab-major
   const DaParts& dp = p.da;
   const int N = dp.N, T = dp.T;
 
@@ -253,9 +255,10 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int ks, int st) {
     const uint32_t lds = lds0 + (uint32_t)(st * STAGE) * 2u;
-    const int k0 = ks * BK;
+    // The weight slab is one contiguous C x 32 block: 1 KB per load instruction.
     slab_issue<C, NW, BK>(
-        lds, wave, K4, [&](int u) { return wt_g + (size_t)(u * NW * 16) * K4 + k0; }, [](int, int i) { return i; });
+        lds, wave, BK, [&](int u) { return wt_g + (size_t)ks * C * BK + (size_t)(u * NW * 16) * BK; },
+        [](int, int i) { return i; });
     {
       const bool tokm = part == 3;
       const bf16_bits* src = da_part(dp, part);
@@ -308,52 +311,79 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
       for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = mfma(af[fb], bfr[tb], acc[fb][tb]);
   }
 
+  // Epilogue. The x block of each wave (its 64 tokens x 128 features, 16 KB)
+  // comes through LDS once the ring is free: 16 direct global->LDS loads of
+  // four whole 256-byte row segments each, chunk c of row r at 16-byte slot
+  // c ^ (r & 15), so the accumulator-layout reads below (lane: one token,
+  // 4 features) are conflict-free. Each wave reads only its own block.
+  __syncthreads();  // every wave is past its last slab read
+  bf16_bits* xs = smem + wave * XW;
+  int mrow[TB];
+  float rxr[TB];
+  {
+    const int r0 = min(m0 + wt * 64, M - 1);
+    const bf16_bits* xb = p.x + (size_t)r0 * C + wf * 128;
+    const uint32_t lds = lds_addr(xs);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = 4 * j + (lane >> 4), ch = (lane & 15) ^ (r & 15);
+      const uint32_t voff = (uint32_t)((min(m0 + wt * 64 + r, M - 1) - r0) * C + ch * 8) * 2u;
+      g2lds16_s(xb, voff, lds + (uint32_t)j * 1024u);
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      mrow[tb] = min(m0 + wt * 64 + tb * 16 + c16, M - 1);
+      rxr[tb] = p.rx[mrow[tb]];
+    }
+  }
+  // Features 16 fb + 4 g .. + 3 of token row r of the wave's block.
+  auto xs_at = [&](int r, int fb) {
+    return reinterpret_cast<u32x2*>(xs + r * 128 + (((2 * fb + (g >> 1)) ^ (r & 15)) << 3) + 4 * (g & 1));
+  };
+  wait_vmcnt0();  // this wave's x block has landed
+
   // acc . x over this wave's 128 features, per token, then across the WF
   // waves that share the tokens.
-  const bf16_bits* xg = p.x;
-  int mrow[TB];
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) {
-    mrow[tb] = min(m0 + wt * 64 + tb * 16 + c16, M - 1);
     float d = 0.f;
 #pragma unroll
     for (int fb = 0; fb < FB; ++fb) {
-      const u32x2 xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + wf * 128 + 16 * fb + 4 * g);
-      d += acc[fb][tb][0] * lo_bf(xv[0]) + acc[fb][tb][1] * hi_bf(xv[0]) + acc[fb][tb][2] * lo_bf(xv[1]) +
-           acc[fb][tb][3] * hi_bf(xv[1]);
+      const u32x2 xw = *xs_at(tb * 16 + c16, fb);
+      d += acc[fb][tb][0] * lo_bf(xw[0]) + acc[fb][tb][1] * hi_bf(xw[0]) + acc[fb][tb][2] * lo_bf(xw[1]) +
+           acc[fb][tb][3] * hi_bf(xw[1]);
     }
     d += shfl_xor(d, 16);
     d += shfl_xor(d, 32);
     if (g == 0) dotp[wf][wt * 64 + tb * 16 + c16] = d;
   }
-  __syncthreads();  // also: every wave is past its last slab read
+  __syncthreads();
 
-  // dx = acc - x rx^2 (acc . x) / C, staged per 16-token block and stored as
-  // whole 256-byte row segments.
-  bf16_bits* stg = smem + wave * 16 * SP;
+  // dx = acc - x rx^2 (acc . x) / C, written over the x values it consumes
+  // (each lane overwrites exactly the 8 bytes it read), then stored per 16
+  // tokens as whole 256-byte row segments.
   const float inv_c = 1.0f / (float)C;
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) {
-    const int tl = wt * 64 + tb * 16 + c16;
     float dot = 0.f;
 #pragma unroll
-    for (int i = 0; i < WF; ++i) dot += dotp[i][tl];
-    const float rxv = p.rx[mrow[tb]];
-    const float cf = rxv * rxv * dot * inv_c;
+    for (int i = 0; i < WF; ++i) dot += dotp[i][wt * 64 + tb * 16 + c16];
+    const float cf = rxr[tb] * rxr[tb] * dot * inv_c;
 #pragma unroll
     for (int fb = 0; fb < FB; ++fb) {
-      const u32x2 xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + wf * 128 + 16 * fb + 4 * g);
+      u32x2* xp = xs_at(tb * 16 + c16, fb);
+      const u32x2 xw = *xp;
       const f32x4& a = acc[fb][tb];
-      const float o0 = a[0] - lo_bf(xv[0]) * cf, o1 = a[1] - hi_bf(xv[0]) * cf;
-      const float o2 = a[2] - lo_bf(xv[1]) * cf, o3 = a[3] - hi_bf(xv[1]) * cf;
-      *reinterpret_cast<u32x2*>(stg + c16 * SP + 16 * fb + 4 * g) = u32x2{pack2(o0, o1), pack2(o2, o3)};
+      const float o0 = a[0] - lo_bf(xw[0]) * cf, o1 = a[1] - hi_bf(xw[0]) * cf;
+      const float o2 = a[2] - lo_bf(xw[1]) * cf, o3 = a[3] - hi_bf(xw[1]) * cf;
+      *xp = u32x2{pack2(o0, o1), pack2(o2, o3)};
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's writes are done
 #pragma unroll
-    for (int it = 0; it < 16 * 16 / 64; ++it) {
-      const int id = lane + 64 * it, row = id >> 4, ch = id & 15;
-      const int m = m0 + wt * 64 + tb * 16 + row;
-      const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * SP + ch * 8);
+    for (int it = 0; it < 4; ++it) {
+      const int r = tb * 16 + it * 4 + (lane >> 4), ch = lane & 15;
+      const int m = m0 + wt * 64 + r;
+      const u32x4 val = *reinterpret_cast<const u32x4*>(xs + r * 128 + ((ch ^ (r & 15)) << 3));
       if (m < M) st16(p.dx + (size_t)m * C + wf * 128 + ch * 8, val);
     }
   }
@@ -389,7 +419,7 @@ __global__ __launch_bounds__(512, 1) void dx_wide_kernel(DxParams p) {
   const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wf = wave;  // one token block of 64: waves run along features only
-  const bf16_bits* wt_g = p.wcatT;  // (C, 4HN)
+  const bf16_bits* wt_g = p.wcatT;  // (4HN / 32, C, 32): k-slab-major
   const DaParts& dp = p.da;
   const int N = dp.N, T = dp.T;
   const int ngroups = (C + CG - 1) / CG;
@@ -418,11 +448,11 @@ __global__ __launch_bounds__(512, 1) void dx_wide_kernel(DxParams p) {
     int part = 0, hh = 0, n0 = 0;
     auto issue = [&](int ks, int st) {
       const uint32_t lds = lds0 + (uint32_t)(st * STAGE) * 2u;
-      const int k0 = ks * BK;
-      // Weight rows f0 .. f0 + CG - 1, clamped to C - 1 (a clamped base keeps
-      // every row offset non-negative).
+      // Weight rows f0 .. f0 + CG - 1 of slab ks, clamped to C - 1 (a clamped
+      // base keeps every row offset non-negative).
+      const bf16_bits* wslab = wt_g + (size_t)ks * C * BK;
       slab_issue<CG, NW, BK>(
-          lds, wave, K4, [&](int u) { return wt_g + (size_t)min(f0 + u * NW * 16, C - 1) * K4 + k0; },
+          lds, wave, BK, [&](int u) { return wslab + (size_t)min(f0 + u * NW * 16, C - 1) * BK; },
           [&](int u, int i) { return min(f0 + u * NW * 16 + i, C - 1) - min(f0 + u * NW * 16, C - 1); });
       {
         const bool tokm = part == 3;
@@ -890,6 +920,50 @@ hipError_t launch_transpose(const bf16_bits* in, int rows, int cols, int ld_in, 
                             int col_off, hipStream_t s) {
   hipLaunchKernelGGL(transpose_kernel, dim3((cols + 63) / 64, (rows + 63) / 64), dim3(256), 0, s, in, rows, cols,
                      ld_in, out, ld_out, col_off);
+  return hipGetLastError();
+}
+
+// Wcat^T in k-slab-major order (the dx A operand): element (f, k) at
+// (k / 32) * C * 32 + f * 32 + k % 32, k indexing the stacked rows of
+// [Wq; Wk; Wv; Wg] (part blockIdx.z, rows z * HN ..). A 64 x 64 tile of one
+// part goes through LDS; each thread writes 16-byte chunks (8 consecutive k
+// of one feature), so every 32-k slab of the tile leaves as 64 contiguous
+// 64-byte rows.
+__global__ __launch_bounds__(256) void wcat_pack_kernel(WcatPackParams p) {
+  __shared__ bf16_bits tile[64][64 + 2];  // [k][f]
+  const int z = blockIdx.z, HN = p.HN, C = p.C;
+  const bf16_bits* in = z == 0 ? p.wq : z == 1 ? p.wk : z == 2 ? p.wv : p.wg;  // (HN, C)
+  const int k0 = blockIdx.y * 64, f0 = blockIdx.x * 64, tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int i = tid + 256 * it, r = i >> 3, c = (i & 7) * 8;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (k0 + r < HN && f0 + c < C) v = ld16(in + (size_t)(k0 + r) * C + f0 + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[r][c + 2 * e] = (bf16_bits)(v[e] & 0xFFFFu);
+      tile[r][c + 2 * e + 1] = (bf16_bits)(v[e] >> 16);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    // i = (slab half s, feature f, chunk ch): consecutive threads write consecutive 16-byte chunks.
+    const int i = tid + 256 * it, s = i >> 8, f = (i >> 2) & 63, ch = i & 3;
+    const int kl = s * 32 + ch * 8;
+    if (k0 + kl >= HN || f0 + f >= C) continue;
+    u32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[e] = (uint32_t)tile[kl + 2 * e][f] | ((uint32_t)tile[kl + 2 * e + 1][f] << 16);
+    const int k = z * HN + k0 + kl;  // HN and k0 are multiples of 32
+    st16(p.out + (size_t)(k >> 5) * C * 32 + (size_t)(f0 + f) * 32 + (k & 31), v);
+  }
+}
+
+hipError_t launch_wcat_pack(const WcatPackParams& p, hipStream_t s) {
+  if (p.HN % 32 != 0 || p.C % 8 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(wcat_pack_kernel, dim3((p.C + 63) / 64, (p.HN + 63) / 64, 4), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -128,7 +128,7 @@ struct DaParts {
 // dx = acc - x * rx^2 * (acc . x) / C.
 struct DxParams {
   DaParts da;
-  const bf16_bits* wcatT;                   // (C, 4*HN)
+  const bf16_bits* wcatT;                   // Wcat^T k-slab-major: (4*HN / 32, C, 32)
   const bf16_bits* x;                       // (M, C)
   const float* rx;                          // (M)
   bf16_bits* dx;                            // (M, C)
@@ -164,6 +164,16 @@ hipError_t launch_dw_reduce(const DwReduceParams& p, hipStream_t s);
 // column col_off.
 hipError_t launch_transpose(const bf16_bits* in, int rows, int cols, int ld_in, bf16_bits* out,
                             int ld_out, int col_off, hipStream_t s);
+
+// Wcat^T for dx in k-slab-major order: element (f, k) at
+// (k / 32) * C * 32 + f * 32 + k % 32, k over the stacked rows of
+// [Wq; Wk; Wv; Wg] (each (HN, C)).
+struct WcatPackParams {
+  const bf16_bits *wq, *wk, *wv, *wg;
+  bf16_bits* out;
+  int HN, C;
+};
+hipError_t launch_wcat_pack(const WcatPackParams& p, hipStream_t s);
 
 // Fills n floats with zero (a kernel, so it is safe inside captured graphs).
 hipError_t launch_zero_f32(float* p, size_t n, hipStream_t s);
