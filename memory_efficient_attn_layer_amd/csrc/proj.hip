@@ -282,12 +282,17 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     constexpr int CPR = N / 8;               // 16-byte chunks per output row
     // Drains the staged block of projection gi for token block tb into
     // dstp + b * bstride + t * tstride.
+    // The lane index the store addresses derive from, opaque to the compiler
+    // inside each tile: hoisted out of the tile loop, those lane-constant
+    // 64-bit offsets would stay live across the main loop and spill.
+    int lane_d = lane;
+    asm volatile("" : "+v"(lane_d));
     auto drain = [&](int gi, int tb, bf16_bits* dstp, size_t bstride, size_t tstride) {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
       bf16_bits* tile0 = dstp + (size_t)b0 * bstride + (size_t)t0 * tstride;  // whole tiles
 #pragma unroll
       for (int it = 0; it < 16 * CPR / 64; ++it) {
-        const int id = lane + 64 * it, row = id / CPR, ch = id % CPR;
+        const int id = lane_d + 64 * it, row = id / CPR, ch = id % CPR;
         const int tl_row = wt * (TB * 16) + tb * 16 + row;
         const u32x4 val = *reinterpret_cast<const u32x4*>(stg + (gi * 16 + row) * SP + ch * 8);
         if (whole) {
