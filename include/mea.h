@@ -30,7 +30,7 @@
  *   - Tensors are dense row-major in the shapes documented per argument.
  *     Pointers must be 16-byte aligned.
  *
- * Supported shapes: N in {64, 128}; C a multiple of 256, C <= 4096; H >= 1;
+ * Supported shapes: N in {64, 128}; C a multiple of 64, 64 <= C <= 4096; H >= 1;
  * B, T >= 1; T <= T_max; and
  * for the backward H * (T + 256) * N < 2^30 (one batch's head-major gradient
  * rows are addressed with 32-bit byte offsets).

@@ -44,8 +44,8 @@ def _validate(x, weights, factor1, factor2, H: int, N: int, eps: float, need_bac
         raise ValueError(f"head width N={N} not supported (supported: {SUPPORTED_HEAD_DIMS})")
     if H < 1:
         raise ValueError(f"H={H} must be >= 1")
-    if C % 256 != 0 or C > MAX_C_FORWARD:
-        raise ValueError(f"model width C={C} must be a multiple of 256 and <= {MAX_C_FORWARD}")
+    if C < 64 or C % 64 != 0 or C > MAX_C_FORWARD:
+        raise ValueError(f"model width C={C} must be a multiple of 64 in [64, {MAX_C_FORWARD}]")
     if need_backward and C > MAX_C_BACKWARD:
         raise ValueError(f"backward supports C <= {MAX_C_BACKWARD}, got C={C}")
     HN = H * N

@@ -64,7 +64,7 @@ int validate(const mea_desc* d, int pass) {
   if (d == nullptr) return MEA_ERR_NULL;
   if (d->B < 1 || d->T < 1 || d->H < 1 || d->T_max < d->T) return MEA_ERR_SHAPE;
   if (d->N != 64 && d->N != 128) return MEA_ERR_HEAD_DIM;
-  if (d->C < 256 || d->C % 256 != 0) return MEA_ERR_MODEL_DIM;
+  if (d->C < 64 || d->C % 64 != 0) return MEA_ERR_MODEL_DIM;
   const bool bwd = pass == MEA_PASS_BWD || pass == MEA_PASS_BWD_TABLES;
   if (d->C > 4096) return MEA_ERR_MODEL_DIM;
   if (!(d->eps > 0.f) || !isfinite(d->eps)) return MEA_ERR_EPS;
@@ -831,7 +831,7 @@ const char* mea_strerror(int code) {
     case MEA_ERR_NULL: return "a required pointer is NULL (or only one of a pair was given)";
     case MEA_ERR_SHAPE: return "B, T, H must be >= 1, T <= T_max, and indices must fit 31 bits";
     case MEA_ERR_HEAD_DIM: return "head width N must be 64 or 128";
-    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 256 and <= 4096";
+    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 64 in [64, 4096]";
     case MEA_ERR_WORKSPACE: return "workspace smaller than mea_workspace_bytes()";
     case MEA_ERR_ALIGN: return "a pointer is not 16-byte aligned";
     case MEA_ERR_EPS: return "eps must be finite and positive";

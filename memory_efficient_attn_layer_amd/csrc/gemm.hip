@@ -22,7 +22,8 @@ namespace mea {
 // y = (O * sig) Wo^T, on the token-block main loop: A = Wo rows (output
 // features, k = HN), B = O * sig rows, gated while the slab is written to
 // LDS. Workgroup (x, y) covers the NF output features from y * NF of BT
-// tokens; y rows leave through an LDS staging block as whole-row segments.
+// tokens (the last group may reach past C); y rows leave through an LDS
+// staging block as whole-row segments.
 // ---------------------------------------------------------------------------
 template <int NF>
 __global__ __launch_bounds__(TokShape<NF>::NT, 1) void gate_oproj_kernel(OprojParams p) {
@@ -33,7 +34,7 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void gate_oproj_kernel(OprojPa
   const int M = p.M, C = p.C, HN = p.HN;
   const int m0 = xcd_remap(blockIdx.x, gridDim.x) * S::BT, f0 = blockIdx.y * NF;
   f32x4 acc[8][4];
-  tok_mainloop<NF, true>(HN, smem, p.wo + (size_t)f0 * HN, HN, NF, p.o, p.sig, HN, m0, M, acc);
+  tok_mainloop<NF, true>(HN, smem, p.wo + (size_t)f0 * HN, HN, min(NF, C - f0), p.o, p.sig, HN, m0, M, acc);
 
   const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
   const int wave = tid >> 6, wf = wave % S::WF, wt = wave / S::WF;
@@ -51,21 +52,23 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void gate_oproj_kernel(OprojPa
       const int id = lane + 64 * it, row = id >> 4, ch = id & 15;
       const int m = m0 + wt * 64 + tb * 16 + row;
       const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * SP + ch * 8);
-      if (m < M) st16(p.y + (size_t)m * C + f0 + wf * 128 + ch * 8, val);
+      if (m < M && f0 + wf * 128 + ch * 8 < C) st16(p.y + (size_t)m * C + f0 + wf * 128 + ch * 8, val);
     }
   }
 }
 
 template <int NF>
 static void launch_oproj_nf(const OprojParams& p, hipStream_t s) {
-  const dim3 grid((p.M + TokShape<NF>::BT - 1) / TokShape<NF>::BT, p.C / NF);
+  const dim3 grid((p.M + TokShape<NF>::BT - 1) / TokShape<NF>::BT, (p.C + NF - 1) / NF);
   hipLaunchKernelGGL(gate_oproj_kernel<NF>, grid, dim3(TokShape<NF>::NT), 0, s, p);
 }
 
 hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s) {
-  if (p.C % 256 != 0 || p.HN % 32 != 0) return hipErrorInvalidValue;
+  if (p.C < 64 || p.C % 64 != 0 || p.HN % 32 != 0) return hipErrorInvalidValue;
   // Feature groups of 512 (or 256): a group of 1024 would shrink the token
-  // block to 64 and re-read all of Wo from L2 for every 64 tokens.
+  // block to 64 and re-read all of Wo from L2 for every 64 tokens. A width
+  // that is no multiple of 256 ends in a partial group (its Wo rows past
+  // C - 1 read row C - 1, its stores stop at C).
   if (p.C == 768)
     launch_oproj_nf<768>(p, s);
   else if (p.C % 512 == 0)
@@ -209,25 +212,30 @@ __device__ __forceinline__ const bf16_bits* da_part(const DaParts& dp, int part)
 // so the RMSNorm backward dot (acc . x) is an in-lane sum, two lane
 // exchanges and a cross-wave sum through LDS; dx rows leave through an LDS
 // staging block as whole-row stores.
+//
+// CP is the padded width the workgroup layout is built for; the model width
+// C = p.C is a multiple of 64 with CP - 256 < C <= CP. Weight rows past C - 1
+// read row C - 1, x columns past the row are clamped into it, accumulators of
+// features past C are zeroed before the dot, and their stores are skipped.
 // ---------------------------------------------------------------------------
-template <int C>
-__global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 128) : 1)), 1) void dx_kernel(DxParams p) {
-  constexpr int WF = C / 128;                           // waves along features
+template <int CP>
+__global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP / 128) : 1)), 1) void dx_kernel(DxParams p) {
+  constexpr int WF = CP / 128;                          // waves along features
   constexpr int WT = 8 % WF == 0 ? 8 / WF : 1;          // waves along tokens
   constexpr int NW = WF * WT;
   constexpr int BT = 64 * WT;                           // tokens per workgroup
-  constexpr int BK = 32, NS = C * 2 <= 1024 ? 3 : 2;    // slab width, ring depth
-  constexpr int STAGE = (C + BT) * BK;
+  constexpr int BK = 32, NS = CP * 2 <= 1024 ? 3 : 2;   // slab width, ring depth
+  constexpr int STAGE = (CP + BT) * BK;
   constexpr int FB = 8, TB = 4;                         // 16-blocks per wave
   // Load instructions every wave issues per slab at least (waves whose
   // share is larger wait for more of their own loads, which is still right).
-  constexpr int LOADS = (C / 16) / NW + (BT / 16) / NW;
+  constexpr int LOADS = (CP / 16) / NW + (BT / 16) / NW;
   constexpr int XW = 64 * 128;                          // x block of one wave (elements)
   constexpr int SMEM = NS * STAGE > NW * XW ? NS * STAGE : NW * XW;
   __shared__ __attribute__((aligned(16))) bf16_bits smem[SMEM];
   __shared__ float dotp[WF][BT];
 
-  const int M = p.M, K4 = 4 * p.HN;
+  const int M = p.M, C = p.C, K4 = 4 * p.HN;
   const int m0 = xcd_remap(blockIdx.x, (M + BT - 1) / BT) * BT;
   const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -255,10 +263,13 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int ks, int st) {
     const uint32_t lds = lds0 + (uint32_t)(st * STAGE) * 2u;
-    // The weight slab is one contiguous C x 32 block: 1 KB per load instruction.
-    slab_issue<C, NW, BK>(
-        lds, wave, BK, [&](int u) { return wt_g + (size_t)ks * C * BK + (size_t)(u * NW * 16) * BK; },
-        [](int, int i) { return i; });
+    // The weight slab is one contiguous C x 32 block: 1 KB per load
+    // instruction (rows past C - 1 read row C - 1; a clamped base keeps every
+    // row offset non-negative).
+    const bf16_bits* wslab = wt_g + (size_t)ks * C * BK;
+    slab_issue<CP, NW, BK>(
+        lds, wave, BK, [&](int u) { return wslab + (size_t)min(u * NW * 16, C - 1) * BK; },
+        [&](int u, int i) { return min(u * NW * 16 + i, C - 1) - min(u * NW * 16, C - 1); });
     {
       const bool tokm = part == 3;
       const bf16_bits* src = da_part(dp, part);
@@ -269,7 +280,7 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
         if (NI % NW != 0 && ins >= NI) break;  // wave-uniform: partial last round
         const size_t off = tokm ? (size_t)mf(u) * dp.ld_g + (hh * N + n0) : ((size_t)hh * T + hmf[u]) * N + n0;
         g2lds16_s(src + off, tokm ? plan_t.voff[u] : plan_h.voff[u],
-                  lds + (uint32_t)(C * BK * 2) + (uint32_t)ins * 1024u);
+                  lds + (uint32_t)(CP * BK * 2) + (uint32_t)ins * 1024u);
       }
     }
     n0 += BK;
@@ -299,7 +310,7 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
     __syncthreads();
     if (ks + NS - 1 < nk) issue(ks + NS - 1, (ks + NS - 1) % NS);
     const bf16_bits* As = smem + (ks % NS) * STAGE;
-    const bf16_bits* Bs = As + C * BK;
+    const bf16_bits* Bs = As + CP * BK;
     bf16x8 af[FB], bfr[TB];
 #pragma unroll
     for (int fb = 0; fb < FB; ++fb) af[fb] = as_frag(slab_read<BK>(As, wf * 128 + fb * 16 + c16, g));
@@ -320,14 +331,25 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
   bf16_bits* xs = smem + wave * XW;
   int mrow[TB];
   float rxr[TB];
+  if (wf * 128 + 128 > C) {
+    // Features 16 fb + 4 g .. + 3 past C: their accumulators (products with
+    // the clamped weight row) must not enter the dot (wave-uniform branch).
+#pragma unroll
+    for (int fb = 0; fb < FB; ++fb) {
+      const bool out = wf * 128 + 16 * fb + 4 * g >= C;
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = out ? zero4() : acc[fb][tb];
+    }
+  }
   {
     const int r0 = min(m0 + wt * 64, M - 1);
-    const bf16_bits* xb = p.x + (size_t)r0 * C + wf * 128;
+    const bf16_bits* xb = p.x + (size_t)r0 * C;
     const uint32_t lds = lds_addr(xs);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int r = 4 * j + (lane >> 4), ch = (lane & 15) ^ (r & 15);
-      const uint32_t voff = (uint32_t)((min(m0 + wt * 64 + r, M - 1) - r0) * C + ch * 8) * 2u;
+      const int col = min(wf * 128 + ch * 8, C - 8);  // columns past the row: clamped, never used
+      const uint32_t voff = (uint32_t)((min(m0 + wt * 64 + r, M - 1) - r0) * C + col) * 2u;
       g2lds16_s(xb, voff, lds + (uint32_t)j * 1024u);
     }
 #pragma unroll
@@ -384,13 +406,13 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
       const int r = tb * 16 + it * 4 + (lane >> 4), ch = lane & 15;
       const int m = m0 + wt * 64 + r;
       const u32x4 val = *reinterpret_cast<const u32x4*>(xs + r * 128 + ((ch ^ (r & 15)) << 3));
-      if (m < M) st16(p.dx + (size_t)m * C + wf * 128 + ch * 8, val);
+      if (m < M && wf * 128 + ch * 8 < C) st16(p.dx + (size_t)m * C + wf * 128 + ch * 8, val);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// dx for C > 1024 (a multiple of 256): the workgroup layout of dx_kernel<1024>
+// dx for C > 1024 (a multiple of 64): the workgroup layout of dx_kernel<1024>
 // (8 waves of 128 features x 64 tokens) walks the output features in groups
 // of 1024. The RMSNorm-backward dot (acc . x) needs the whole row, so it is
 // summed over the groups in LDS; every group but the last leaves its
@@ -399,9 +421,9 @@ __global__ __launch_bounds__(64 * ((C / 128) * (8 % (C / 128) == 0 ? 8 / (C / 12
 // earlier groups, applies the correction and writes them back (a thread's
 // own store is visible to its own later load once vmcnt has drained; no
 // other workgroup touches these rows, and da_g does not live in dx here).
-// Weight rows past C are clamped on load; a wave's 128-feature slice is then
-// either wholly inside C or wholly past it (C and the groups are multiples
-// of 128) and the latter stores nothing.
+// Weight rows past C are clamped on load. Only the last group can reach past
+// C: there features from C on read no x, add nothing to the dot and store
+// nothing (a wave's slice wholly past C skips its loads and stores).
 // ---------------------------------------------------------------------------
 constexpr int kDxGroup = 1024;
 
@@ -510,7 +532,9 @@ __global__ __launch_bounds__(512, 1) void dx_wide_kernel(DxParams p) {
       if (wave_live) {
 #pragma unroll
         for (int fb = 0; fb < FB; ++fb) {
-          const u32x2 xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + f0 + wf * 128 + 16 * fb + 4 * g);
+          const int f = f0 + wf * 128 + 16 * fb + 4 * g;
+          if (f >= C) continue;
+          const u32x2 xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + f);
           d += acc[fb][tb][0] * lo_bf(xv[0]) + acc[fb][tb][1] * hi_bf(xv[0]) + acc[fb][tb][2] * lo_bf(xv[1]) +
                acc[fb][tb][3] * hi_bf(xv[1]);
         }
@@ -539,8 +563,8 @@ __global__ __launch_bounds__(512, 1) void dx_wide_kernel(DxParams p) {
 #pragma unroll
       for (int fb = 0; fb < FB; ++fb) {
         u32x2 xv = {0u, 0u};
-        if (last && wave_live)
-          xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + f0 + wf * 128 + 16 * fb + 4 * g);
+        const int f = f0 + wf * 128 + 16 * fb + 4 * g;
+        if (last && f < C) xv = *reinterpret_cast<const u32x2*>(xg + (size_t)mrow[tb] * C + f);
         const f32x4& a = acc[fb][tb];
         const float o0 = a[0] - lo_bf(xv[0]) * cf, o1 = a[1] - hi_bf(xv[0]) * cf;
         const float o2 = a[2] - lo_bf(xv[1]) * cf, o3 = a[3] - hi_bf(xv[1]) * cf;
@@ -552,7 +576,7 @@ __global__ __launch_bounds__(512, 1) void dx_wide_kernel(DxParams p) {
         const int id = lane + 64 * it, row = id >> 4, ch = id & 15;
         const int m = m0 + tb * 16 + row;
         const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * SP + ch * 8);
-        if (m < M && wave_live) st16(p.dx + (size_t)m * C + f0 + wf * 128 + ch * 8, val);
+        if (m < M && f0 + wf * 128 + ch * 8 < C) st16(p.dx + (size_t)m * C + f0 + wf * 128 + ch * 8, val);
       }
     }
     __syncthreads();  // the staging area is the next group's slab ring
@@ -584,23 +608,19 @@ __global__ __launch_bounds__(512, 1) void dx_wide_kernel(DxParams p) {
 }
 
 hipError_t launch_dx(const DxParams& p, hipStream_t s) {
-  switch (p.C) {
-    case 256:
-      hipLaunchKernelGGL(dx_kernel<256>, dim3((p.M + 255) / 256), dim3(512), 0, s, p);
-      break;
-    case 512:
-      hipLaunchKernelGGL(dx_kernel<512>, dim3((p.M + 127) / 128), dim3(512), 0, s, p);
-      break;
-    case 768:
-      hipLaunchKernelGGL(dx_kernel<768>, dim3((p.M + 63) / 64), dim3(384), 0, s, p);
-      break;
-    case 1024:
-      hipLaunchKernelGGL(dx_kernel<1024>, dim3((p.M + 63) / 64), dim3(512), 0, s, p);
-      break;
-    default:
-      if (p.C <= 1024 || p.C % 256 != 0) return hipErrorInvalidValue;
-      hipLaunchKernelGGL(dx_wide_kernel, dim3((p.M + 63) / 64), dim3(512), 0, s, p);
-  }
+  // Model widths are multiples of 64; a width runs on the smallest padded
+  // layout that holds it, widths past 1024 on the feature-group kernel.
+  if (p.C < 64 || p.C % 64 != 0) return hipErrorInvalidValue;
+  if (p.C <= 256)
+    hipLaunchKernelGGL(dx_kernel<256>, dim3((p.M + 255) / 256), dim3(512), 0, s, p);
+  else if (p.C <= 512)
+    hipLaunchKernelGGL(dx_kernel<512>, dim3((p.M + 127) / 128), dim3(512), 0, s, p);
+  else if (p.C <= 768)
+    hipLaunchKernelGGL(dx_kernel<768>, dim3((p.M + 63) / 64), dim3(384), 0, s, p);
+  else if (p.C <= 1024)
+    hipLaunchKernelGGL(dx_kernel<1024>, dim3((p.M + 63) / 64), dim3(512), 0, s, p);
+  else
+    hipLaunchKernelGGL(dx_wide_kernel, dim3((p.M + 63) / 64), dim3(512), 0, s, p);
   return hipGetLastError();
 }
 
@@ -709,8 +729,9 @@ __global__ __launch_bounds__(512, 1) void dw_partial_kernel(DwParams p) {
   constexpr int STAGES = 3;
   __shared__ __attribute__((aligned(16))) bf16_bits smem[STAGES * 2 * kDwSlab];
   const int M = p.M, C = p.C, HN = p.HN, K4 = 4 * HN;
-  const int t0 = (K4 / kDwTile) * (C / kDwTile);           // problem-0 tiles
-  const int t1 = (C / kDwTile) * ((HN + kDwTile - 1) / kDwTile);
+  const int nc = (C + kDwTile - 1) / kDwTile;              // tiles along C (the last may be partial)
+  const int t0 = (K4 / kDwTile) * nc;                       // problem-0 tiles
+  const int t1 = nc * ((HN + kDwTile - 1) / kDwTile);
   const int ntile = t0 + t1;
   // Consecutive logical ids (same token split, neighbouring tiles) share an
   // XCD, so the operand rows of a split are fetched into one L2.
@@ -718,7 +739,7 @@ __global__ __launch_bounds__(512, 1) void dw_partial_kernel(DwParams p) {
   const int z = L / ntile, tile = L - z * ntile;
   const bool prob1 = tile >= t0;
   const int lt = prob1 ? tile - t0 : tile;
-  const int ntj = prob1 ? (HN + kDwTile - 1) / kDwTile : C / kDwTile;
+  const int ntj = prob1 ? (HN + kDwTile - 1) / kDwTile : nc;
   const int i0 = (lt / ntj) * kDwTile, j0 = (lt % ntj) * kDwTile;
   const int I = prob1 ? C : K4, J = prob1 ? HN : C;
   const bf16_bits* bsrc = prob1 ? p.z : p.x;
@@ -734,7 +755,7 @@ __global__ __launch_bounds__(512, 1) void dw_partial_kernel(DwParams p) {
 
   // A slabs (this lane: rows 2 * ins + lane / 32, ins = 8u + wave; column
   // chunk as in dw_issue). Slabs are issued in order s = 0, 1, 2, ...
-  //  FAST (T a multiple of kDwBK, HN of kDwTile; then every token chunk is a
+  //  FAST (T a multiple of kDwBK, HN and C of kDwTile; then every token chunk is a
   //  multiple of kDwBK): no slab crosses a sequence or runs past M and the
   //  tile's columns lie in one part, so slab s reads from the uniform base
   //  asrc + arow * ald, arow being the row of its first token (head-major
@@ -845,8 +866,14 @@ __global__ __launch_bounds__(512, 1) void dw_partial_kernel(DwParams p) {
     }
 }
 
+// Output tiles of both problems (tiles along C rounded up).
+static int dw_tiles(int C, int HN) {
+  const int nc = (C + kDwTile - 1) / kDwTile;
+  return (4 * HN / kDwTile) * nc + nc * ((HN + kDwTile - 1) / kDwTile);
+}
+
 int dw_splits(int M, int C, int HN) {
-  const int tiles = (4 * HN / kDwTile) * (C / kDwTile) + (C / kDwTile) * ((HN + kDwTile - 1) / kDwTile);
+  const int tiles = dw_tiles(C, HN);
   static int cus = 0;
   if (cus == 0) {
     int dev = 0, n = 0;
@@ -862,8 +889,10 @@ int dw_splits(int M, int C, int HN) {
 }
 
 hipError_t launch_dw_partial(const DwParams& p, hipStream_t s) {
-  const int tiles = (4 * p.HN / kDwTile) * (p.C / kDwTile) + (p.C / kDwTile) * ((p.HN + kDwTile - 1) / kDwTile);
-  if (p.da.T % kDwBK == 0 && p.HN % kDwTile == 0)
+  if (p.C % 64 != 0 || (4 * p.HN) % kDwTile != 0) return hipErrorInvalidValue;
+  const int tiles = dw_tiles(p.C, p.HN);
+  // The fast path reads dy's columns unclamped: whole tiles along C only.
+  if (p.da.T % kDwBK == 0 && p.HN % kDwTile == 0 && p.C % kDwTile == 0)
     hipLaunchKernelGGL(dw_partial_kernel<true>, dim3(tiles * p.splits), dim3(512), 0, s, p);
   else
     hipLaunchKernelGGL(dw_partial_kernel<false>, dim3(tiles * p.splits), dim3(512), 0, s, p);

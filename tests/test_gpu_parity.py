@@ -107,6 +107,15 @@ BLOCK_CASES = [
     ("c1280-h5-b2-t100", _w("c1280", 2, 100, 1280, 5, 64), None),
     ("c2048-h16-n128-yarn8-b1-t256", _w("c2048", 1, 256, 2048, 16, 128, 8.0, 64), None),
     ("c3072-h4-b1-t64", _w("c3072", 1, 64, 3072, 4, 64), None),
+    # C a multiple of 64 but not of 256 (any head count H at C = H*N): dx runs
+    # the next wider layout with the features past C masked, the output
+    # projection and dW end in partial 256-feature tiles.
+    ("c384-h6-b2-t130", _w("c384", 2, 130, 384, 6, 64), None),
+    ("c640-h5-n128-b1-t200", _w("c640", 1, 200, 640, 5, 128), None),
+    ("c192-h3-b2-t90", _w("c192", 2, 90, 192, 3, 64), None),
+    ("c64-h1-b2-t100", _w("c64", 2, 100, 64, 1, 64), None),
+    ("c320-ne-hn-h2-n128-b1-t64", _w("c320", 1, 64, 320, 2, 128), None),
+    ("c1344-h21-b1-t80", _w("c1344", 1, 80, 1344, 21, 64), None),
 ]
 
 

@@ -82,7 +82,8 @@ def test_workspace_bytes(lib):
     "kw,code",
     [
         (dict(N=32), "MEA_ERR_HEAD_DIM"),
-        (dict(C=384), "MEA_ERR_MODEL_DIM"),
+        (dict(C=352), "MEA_ERR_MODEL_DIM"),
+        (dict(C=32), "MEA_ERR_MODEL_DIM"),
         (dict(T_max=100), "MEA_ERR_SHAPE"),
         (dict(H=0), "MEA_ERR_SHAPE"),
         (dict(eps=-1.0), "MEA_ERR_EPS"),
