@@ -30,7 +30,8 @@
  *   - Tensors are dense row-major in the shapes documented per argument.
  *     Pointers must be 16-byte aligned.
  *
- * Supported shapes: N in {64, 128}; C a multiple of 64, 64 <= C <= 4096; H >= 1;
+ * Supported shapes: N in {64, 128} (heads of 16 or 32 dimensions zero-padded
+ * to N = 64, see N_active); C a multiple of 32, 32 <= C <= 4096; H >= 1;
  * B, T >= 1; T <= T_max; and
  * for the backward H * (T + 256) * N < 2^30 (one batch's head-major gradient
  * rows are addressed with 32-bit byte offsets).
@@ -54,6 +55,13 @@ typedef struct mea_desc {
   int64_t N;      /* head width */
   int64_t T_max;  /* rows of the rotary tables, >= T */
   float eps;      /* RMSNorm epsilon; the reference default is 1e-6 (fast_triton_attn.py:681) */
+  int64_t N_active; /* head dimensions in use: 0 (all N), or 16 or 32 with N = 64.
+                       No counterpart in the reference: a head of N_active < N
+                       dimensions is carried zero-padded to N (the last
+                       N - N_active rows of every head in Wq, Wk, Wv, Wg, columns
+                       in Wo and in the rotary tables are zero); the head
+                       RMSNorm then averages over N_active dimensions and the
+                       attention scale is 1/sqrt(N_active). */
 } mea_desc;
 
 enum {

@@ -33,6 +33,7 @@ class MeaDesc(ctypes.Structure):
         ("N", ctypes.c_int64),
         ("T_max", ctypes.c_int64),
         ("eps", ctypes.c_float),
+        ("N_active", ctypes.c_int64),
     ]
 
 
@@ -121,8 +122,9 @@ def check(code: int, what: str) -> None:
         raise RuntimeError(f"{what} failed: {strerror(code)} (status {code})")
 
 
-def desc(B: int, T: int, C: int, H: int, N: int, T_max: int, eps: float) -> MeaDesc:
-    return MeaDesc(int(B), int(T), int(C), int(H), int(N), int(T_max), float(eps))
+def desc(B: int, T: int, C: int, H: int, N: int, T_max: int, eps: float, N_active: int = 0) -> MeaDesc:
+    """A descriptor; N_active > 0: heads of N_active dimensions carried zero-padded to N."""
+    return MeaDesc(int(B), int(T), int(C), int(H), int(N), int(T_max), float(eps), int(N_active))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

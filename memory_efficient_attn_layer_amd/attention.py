@@ -20,6 +20,10 @@ Differences from the reference, all deliberate:
   * Rotary tables may be bf16, fp16 or fp32 (the reference accepts only bf16).
   * Without a gradient requirement the forward keeps no activations.
   * Unsupported shapes raise ValueError before any launch.
+  * Heads of 16 or 32 dimensions run zero-padded to 64 (zero weight rows
+    and o_proj columns, identity rotary pairs); the head RMSNorm and the
+    attention scale use the true head width, so results are those of the
+    unpadded block, at the cost of the padded width.
 """
 from __future__ import annotations
 
@@ -27,7 +31,9 @@ import torch
 
 from . import _lib
 
-SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_HEAD_DIMS = (16, 32, 64, 128)
+PADDED_HEAD_DIMS = (16, 32)  # carried zero-padded to PAD_N dimensions
+PAD_N = 64
 MAX_C_FORWARD = 4096
 MAX_C_BACKWARD = 4096
 
@@ -44,8 +50,8 @@ def _validate(x, weights, factor1, factor2, H: int, N: int, eps: float, need_bac
         raise ValueError(f"head width N={N} not supported (supported: {SUPPORTED_HEAD_DIMS})")
     if H < 1:
         raise ValueError(f"H={H} must be >= 1")
-    if C < 64 or C % 64 != 0 or C > MAX_C_FORWARD:
-        raise ValueError(f"model width C={C} must be a multiple of 64 in [64, {MAX_C_FORWARD}]")
+    if C < 32 or C % 32 != 0 or C > MAX_C_FORWARD:
+        raise ValueError(f"model width C={C} must be a multiple of 32 in [32, {MAX_C_FORWARD}]")
     if need_backward and C > MAX_C_BACKWARD:
         raise ValueError(f"backward supports C <= {MAX_C_BACKWARD}, got C={C}")
     HN = H * N
@@ -75,6 +81,26 @@ def _validate(x, weights, factor1, factor2, H: int, N: int, eps: float, need_bac
         raise RuntimeError("fused_attn runs only on a ROCm GPU device (there is no CPU path)")
 
 
+def _pad_heads(H: int, N: int, weights, factor1, factor2):
+    """Zero-pads every head from N to PAD_N dimensions, differentiably (the
+    gradients of the caller's tensors are the slices of the padded ones):
+    rows of Wq, Wk, Wv, Wg and columns of Wo get zeros; the rotary tables get
+    identity pairs (factor1 = 1, factor2 = 0), which keep the padded q and k
+    dimensions at zero and the pair blocks invertible for the backward."""
+    wq, wk, wv, wg, wo = weights
+    P = PAD_N - N
+
+    def rows(w):
+        C = w.shape[1]
+        return torch.cat([w.reshape(H, N, C), w.new_zeros(H, P, C)], dim=1).reshape(H * PAD_N, C)
+
+    C = wo.shape[0]
+    wo_p = torch.cat([wo.reshape(C, H, N), wo.new_zeros(C, H, P)], dim=2).reshape(C, H * PAD_N)
+    f1_p = torch.cat([factor1, factor1.new_ones(factor1.shape[0], P)], dim=1)
+    f2_p = torch.cat([factor2, factor2.new_zeros(factor2.shape[0], P)], dim=1)
+    return (rows(wq), rows(wk), rows(wv), rows(wg), wo_p), f1_p, f2_p
+
+
 def _tables32(factor1: torch.Tensor, factor2: torch.Tensor, T: int):
     return factor1[:T].float().contiguous(), factor2[:T].float().contiguous()
 
@@ -98,11 +124,18 @@ class FusedAttentionFunction(torch.autograd.Function):
     @classmethod
     def apply(cls, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H, N, eps=1e-6):
         save = _wants_grad(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2)
-        return super().apply(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H, N, eps, save)
+        weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
+        H, N = int(H), int(N)
+        if N in PADDED_HEAD_DIMS:
+            _validate(x, weights, factor1, factor2, H, N, float(eps), save)
+            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2)
+            return super().apply(x, *weights, factor1, factor2, H, PAD_N, eps, save, N)
+        return super().apply(x, *weights, factor1, factor2, H, N, eps, save, 0)
 
     @staticmethod
-    def forward(ctx, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H, N, eps, save):
-        H, N, eps = int(H), int(N), float(eps)
+    def forward(ctx, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, H, N, eps, save,
+                n_active):
+        H, N, eps, n_active = int(H), int(N), float(eps), int(n_active)
         weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
         need_bwd = bool(save)
         _validate(x, weights, factor1, factor2, H, N, eps, need_bwd)
@@ -112,7 +145,7 @@ class FusedAttentionFunction(torch.autograd.Function):
         xc = x.contiguous()
         wc = [w.contiguous() for w in weights]
         f1, f2 = _tables32(factor1, factor2, T)
-        d = _lib.desc(B, T, C, H, N, T, eps)
+        d = _lib.desc(B, T, C, H, N, T, eps, n_active)
         y = torch.empty((B, T, C), device=dev, dtype=torch.bfloat16)
         if need_bwd:
             o_save = torch.empty((B, T, H * N), device=dev, dtype=torch.bfloat16)
@@ -129,7 +162,7 @@ class FusedAttentionFunction(torch.autograd.Function):
         _lib.check(rc, "mea_fwd")
         if need_bwd:
             ctx.save_for_backward(xc, *wc, factor1, factor2, o_save, lse)
-        ctx.H, ctx.N, ctx.eps = H, N, eps
+        ctx.H, ctx.N, ctx.eps, ctx.n_active = H, N, eps, n_active
         return y
 
     @staticmethod
@@ -141,7 +174,7 @@ class FusedAttentionFunction(torch.autograd.Function):
         dev = x.device
         dy = grad_output.to(torch.bfloat16).contiguous()
         f1, f2 = _tables32(factor1, factor2, T)
-        d = _lib.desc(B, T, C, H, N, T, eps)
+        d = _lib.desc(B, T, C, H, N, T, eps, ctx.n_active)
         dx = torch.empty_like(x)
         dws = [torch.empty_like(w) for w in (wq, wk, wv, wg, wo)]
         want_f = ctx.needs_input_grad[6] or ctx.needs_input_grad[7]
@@ -167,7 +200,7 @@ class FusedAttentionFunction(torch.autograd.Function):
             gf2 = torch.zeros_like(factor2)
             gf1[:T] = df1.to(factor1.dtype)
             gf2[:T] = df2.to(factor2.dtype)
-        return (dx, *dws, gf1, gf2, None, None, None, None)
+        return (dx, *dws, gf1, gf2, None, None, None, None, None)
 
 
 def fused_attn(x, q_proj, k_proj, v_proj, g_proj, o_proj, yarn_module, H, N, eps=1e-6):
@@ -200,13 +233,20 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
     def apply(cls, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, cu_seqlens, max_len, H, N,
               eps=1e-6):
         save = _wants_grad(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2)
-        return super().apply(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, cu_seqlens,
-                             max_len, H, N, eps, save)
+        weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
+        H, N = int(H), int(N)
+        if N in PADDED_HEAD_DIMS:
+            if not isinstance(x, torch.Tensor) or x.dim() != 2:
+                raise ValueError("x must be a (total_tokens, C) tensor")
+            _validate(x[:1].unsqueeze(0), weights, factor1, factor2, H, N, float(eps), save)
+            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2)
+            return super().apply(x, *weights, factor1, factor2, cu_seqlens, max_len, H, PAD_N, eps, save, N)
+        return super().apply(x, *weights, factor1, factor2, cu_seqlens, max_len, H, N, eps, save, 0)
 
     @staticmethod
     def forward(ctx, x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2, cu_seqlens, max_len, H,
-                N, eps, save):
-        H, N, eps, max_len = int(H), int(N), float(eps), int(max_len)
+                N, eps, save, n_active):
+        H, N, eps, max_len, n_active = int(H), int(N), float(eps), int(max_len), int(n_active)
         weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
         if not isinstance(x, torch.Tensor) or x.dim() != 2:
             raise ValueError("x must be a (total_tokens, C) tensor")
@@ -228,8 +268,8 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         wc = [w.contiguous() for w in weights]
         cu = cu_seqlens.contiguous()
         f1, f2 = _tables32(factor1, factor2, max_len)
-        d = _lib.desc(1, total, C, H, N, max_len, eps)
-        d_ws = _lib.desc(1, total, C, H, N, total, eps)
+        d = _lib.desc(1, total, C, H, N, max_len, eps, n_active)
+        d_ws = _lib.desc(1, total, C, H, N, total, eps, n_active)
         y = torch.empty((total, C), device=dev, dtype=torch.bfloat16)
         if need_bwd:
             o_save = torch.empty((total, H * N), device=dev, dtype=torch.bfloat16)
@@ -247,7 +287,7 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         _lib.check(rc, "mea_fwd_varlen")
         if need_bwd:
             ctx.save_for_backward(xc, *wc, factor1, factor2, cu, o_save, lse)
-        ctx.H, ctx.N, ctx.eps, ctx.max_len = H, N, eps, max_len
+        ctx.H, ctx.N, ctx.eps, ctx.max_len, ctx.n_active = H, N, eps, max_len, n_active
         return y
 
     @staticmethod
@@ -262,8 +302,8 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         nseq = cu.numel() - 1
         dy = grad_output.to(torch.bfloat16).contiguous()
         f1, f2 = _tables32(factor1, factor2, max_len)
-        d = _lib.desc(1, total, C, H, N, max_len, eps)
-        d_ws = _lib.desc(1, total, C, H, N, total, eps)
+        d = _lib.desc(1, total, C, H, N, max_len, eps, ctx.n_active)
+        d_ws = _lib.desc(1, total, C, H, N, total, eps, ctx.n_active)
         dx = torch.empty_like(x)
         dws = [torch.empty_like(w) for w in (wq, wk, wv, wg, wo)]
         want_f = ctx.needs_input_grad[6] or ctx.needs_input_grad[7]
@@ -288,7 +328,7 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
             gf2 = torch.zeros_like(factor2)
             gf1[:max_len] = df1.to(factor1.dtype)
             gf2[:max_len] = df2.to(factor2.dtype)
-        return (dx, *dws, gf1, gf2, None, None, None, None, None, None)
+        return (dx, *dws, gf1, gf2, None, None, None, None, None, None, None)
 
 
 def fused_attn_varlen(x, q_proj, k_proj, v_proj, g_proj, o_proj, yarn_module, H, N, cu_seqlens, max_len=None,

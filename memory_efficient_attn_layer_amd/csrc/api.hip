@@ -64,7 +64,9 @@ int validate(const mea_desc* d, int pass) {
   if (d == nullptr) return MEA_ERR_NULL;
   if (d->B < 1 || d->T < 1 || d->H < 1 || d->T_max < d->T) return MEA_ERR_SHAPE;
   if (d->N != 64 && d->N != 128) return MEA_ERR_HEAD_DIM;
-  if (d->C < 64 || d->C % 64 != 0) return MEA_ERR_MODEL_DIM;
+  if (d->N_active != 0 && d->N_active != d->N && !(d->N == 64 && (d->N_active == 16 || d->N_active == 32)))
+    return MEA_ERR_HEAD_DIM;
+  if (d->C < 32 || d->C % 32 != 0) return MEA_ERR_MODEL_DIM;
   const bool bwd = pass == MEA_PASS_BWD || pass == MEA_PASS_BWD_TABLES;
   if (d->C > 4096) return MEA_ERR_MODEL_DIM;
   if (!(d->eps > 0.f) || !isfinite(d->eps)) return MEA_ERR_EPS;
@@ -196,6 +198,8 @@ namespace {
 // log2(e)/sqrt(N): the block stores q in these units, so the attention's
 // logits come out of the MFMA ready for exp2.
 float q_log2_scale(int64_t N) { return (float)(1.4426950408889634 / sqrt((double)N)); }
+// Head dimensions in use (the rest of each head is zero padding).
+int64_t n_active(const mea_desc* d) { return d->N_active != 0 ? d->N_active : d->N; }
 
 // Launch sequence pieces; the public entry points validate before calling.
 int proj_launch(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
@@ -225,6 +229,7 @@ int proj_launch(const mea_desc* d, const void* x, const void* wq, const void* wk
   p.C = (int)d->C;
   p.H = (int)d->H;
   p.eps = d->eps;
+  p.inv_n = 1.0f / (float)n_active(d);
   hipStream_t s = static_cast<hipStream_t>(stream);
   MEA_TRY(timed(K_QKVG_PROJ, s, [&] { return mea::launch_qkvg_proj(p, (int)d->N, s); }));
   return MEA_OK;
@@ -304,7 +309,7 @@ extern "C" {
 
 int mea_attn_fwd(const mea_desc* d, const void* q, const void* k, const void* v, void* o, float* lse,
                  void* stream) {
-  return attn_fwd_impl(d, q, k, v, o, lse, q_log2_scale(d->N), nullptr, stream);
+  return attn_fwd_impl(d, q, k, v, o, lse, q_log2_scale(n_active(d)), nullptr, stream);
 }
 
 int mea_gate_oproj(const mea_desc* d, const void* o, const void* sig, const void* wo, void* y, void* stream) {
@@ -340,7 +345,7 @@ int fwd_impl(const mea_desc* d, const Varlen* var, const void* x, const void* wq
   float* qkn = at<float>(ws, L.qkn);
   MEA_TRY(timed(K_ZERO, static_cast<hipStream_t>(stream),
                 [&] { return mea::launch_zero_f32(qkn, 2, static_cast<hipStream_t>(stream)); }));
-  const float qs = q_log2_scale(d->N);
+  const float qs = q_log2_scale(n_active(d));
   int* tpos = nullptr;
   if (var != nullptr) {
     tpos = at<int>(ws, L.tpos);
@@ -402,7 +407,7 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
     MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_wcat_pack(wp, s); }));
   }
   // Recompute q, k, v, sigmoid(g) and the three RMS statistics.
-  const float qs = q_log2_scale(N);
+  const float qs = q_log2_scale(n_active(d));
   int* tpos = nullptr;
   if (var != nullptr) {
     tpos = at<int>(ws, L.tpos);
@@ -449,9 +454,10 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
   ab.B = (int)d->B;
   ab.H = H;
   ab.T = T;
-  ab.scale = (float)(1.0 / sqrt((double)N));
+  ab.scale = (float)(1.0 / sqrt((double)n_active(d)));
   ab.sl2e = 1.0f;  // q was stored in log2 units by the recompute above
   ab.qscale = qs;
+  ab.inv_n = 1.0f / (float)n_active(d);
   ab.cu = var != nullptr ? var->cu : nullptr;
   ab.nseq = var != nullptr ? var->nseq : 0;
   ab.max_len = var != nullptr ? var->max_len : 0;
@@ -730,7 +736,8 @@ int decode_launch(const mea_desc* d, const void* x, const void* wq, const void* 
   pp.H = (int)d->H;
   pp.t_max = (int)d->T_max;
   pp.eps = d->eps;
-  pp.qscale = q_log2_scale(N);
+  pp.qscale = q_log2_scale(n_active(d));
+  pp.inv_n = 1.0f / (float)n_active(d);
   MEA_TRY(timed(K_DECODE_PROJ, s, [&] { return mea::launch_decode_proj_epilogue(pp, N, s); }));
   mea::DecodeParams dp;
   dp.q = q;
@@ -831,7 +838,7 @@ const char* mea_strerror(int code) {
     case MEA_ERR_NULL: return "a required pointer is NULL (or only one of a pair was given)";
     case MEA_ERR_SHAPE: return "B, T, H must be >= 1, T <= T_max, and indices must fit 31 bits";
     case MEA_ERR_HEAD_DIM: return "head width N must be 64 or 128";
-    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 64 in [64, 4096]";
+    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 32 in [32, 4096]";
     case MEA_ERR_WORKSPACE: return "workspace smaller than mea_workspace_bytes()";
     case MEA_ERR_ALIGN: return "a pointer is not 16-byte aligned";
     case MEA_ERR_EPS: return "eps must be finite and positive";

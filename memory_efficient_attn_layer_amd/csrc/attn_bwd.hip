@@ -118,7 +118,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
         dot += shfl_xor(dot, 4);
         if (CPR == 16) dot += shfl_xor(dot, 8);
         const float rr = rrw[k];
-        const float sc = rxv * rr, cf = dot / (float)N;
+        const float sc = rxv * rr, cf = dot * p.inv_n;
 #pragma unroll
         for (int i = 0; i < 8; ++i) res[i] = sc * (dh[i] - xh[i] * cf);
         if (TG && valid) {

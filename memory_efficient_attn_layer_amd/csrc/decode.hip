@@ -282,8 +282,8 @@ __global__ __launch_bounds__(N) void decode_proj_epilogue_kernel(DecodeProjParam
   const float rx = rsqrtf(block_sum<N>(ss, red) / (float)p.C + p.eps);
   const float* a = p.a + (size_t)b * 4 * HN + h * N + n;
   const float aq = a[0] * rx, ak = a[HN] * rx, av = a[2 * HN] * rx, ag = a[3 * HN] * rx;
-  const float rq = rsqrtf(block_sum<N>(aq * aq, red) / (float)N + p.eps);
-  const float rk = rsqrtf(block_sum<N>(ak * ak, red) / (float)N + p.eps);
+  const float rq = rsqrtf(block_sum<N>(aq * aq, red) * p.inv_n + p.eps);
+  const float rk = rsqrtf(block_sum<N>(ak * ak, red) * p.inv_n + p.eps);
   const float qh = aq * rq, kh = ak * rk;
   const int row = min(max(p.pos[b], 0), p.t_max - 1);
   const float f1 = p.f1[(size_t)row * N + n], f2 = p.f2[(size_t)row * N + n];

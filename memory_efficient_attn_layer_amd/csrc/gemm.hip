@@ -64,7 +64,7 @@ static void launch_oproj_nf(const OprojParams& p, hipStream_t s) {
 }
 
 hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s) {
-  if (p.C < 64 || p.C % 64 != 0 || p.HN % 32 != 0) return hipErrorInvalidValue;
+  if (p.C < 32 || p.C % 32 != 0 || p.HN % 32 != 0) return hipErrorInvalidValue;
   // Feature groups of 512 (or 256): a group of 1024 would shrink the token
   // block to 64 and re-read all of Wo from L2 for every 64 tokens. A width
   // that is no multiple of 256 ends in a partial group (its Wo rows past
@@ -214,7 +214,7 @@ __device__ __forceinline__ const bf16_bits* da_part(const DaParts& dp, int part)
 // staging block as whole-row stores.
 //
 // CP is the padded width the workgroup layout is built for; the model width
-// C = p.C is a multiple of 64 with CP - 256 < C <= CP. Weight rows past C - 1
+// C = p.C is a multiple of 32 with CP - 256 < C <= CP. Weight rows past C - 1
 // read row C - 1, x columns past the row are clamped into it, accumulators of
 // features past C are zeroed before the dot, and their stores are skipped.
 // ---------------------------------------------------------------------------
@@ -412,7 +412,7 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
 }
 
 // ---------------------------------------------------------------------------
-// dx for C > 1024 (a multiple of 64): the workgroup layout of dx_kernel<1024>
+// dx for C > 1024 (a multiple of 32): the workgroup layout of dx_kernel<1024>
 // (8 waves of 128 features x 64 tokens) walks the output features in groups
 // of 1024. The RMSNorm-backward dot (acc . x) needs the whole row, so it is
 // summed over the groups in LDS; every group but the last leaves its
@@ -608,9 +608,9 @@ __global__ __launch_bounds__(512, 1) void dx_wide_kernel(DxParams p) {
 }
 
 hipError_t launch_dx(const DxParams& p, hipStream_t s) {
-  // Model widths are multiples of 64; a width runs on the smallest padded
+  // Model widths are multiples of 32; a width runs on the smallest padded
   // layout that holds it, widths past 1024 on the feature-group kernel.
-  if (p.C < 64 || p.C % 64 != 0) return hipErrorInvalidValue;
+  if (p.C < 32 || p.C % 32 != 0) return hipErrorInvalidValue;
   if (p.C <= 256)
     hipLaunchKernelGGL(dx_kernel<256>, dim3((p.M + 255) / 256), dim3(512), 0, s, p);
   else if (p.C <= 512)
@@ -889,7 +889,7 @@ int dw_splits(int M, int C, int HN) {
 }
 
 hipError_t launch_dw_partial(const DwParams& p, hipStream_t s) {
-  if (p.C % 64 != 0 || (4 * p.HN) % kDwTile != 0) return hipErrorInvalidValue;
+  if (p.C % 32 != 0 || (4 * p.HN) % kDwTile != 0) return hipErrorInvalidValue;
   const int tiles = dw_tiles(p.C, p.HN);
   // The fast path reads dy's columns unclamped: whole tiles along C only.
   if (p.da.T % kDwBK == 0 && p.HN % kDwTile == 0 && p.C % kDwTile == 0)

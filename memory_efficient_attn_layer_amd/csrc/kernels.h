@@ -28,6 +28,7 @@ struct ProjParams {
   int M, T, C, H;
   float eps;
   float qscale;                             // the stored q rows are q * qscale
+  float inv_n;                              // 1 / head dimensions in use (head RMSNorm mean)
 };
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s);
 
@@ -77,6 +78,7 @@ struct AttnBwdParams {
   float scale;                              // softmax scale 1/sqrt(N)
   float sl2e;                               // must be 1: stored q . k is in log2 units
   float qscale;                             // stored q = q * qscale
+  float inv_n;                              // 1 / head dimensions in use (head RMSNorm mean)
   const int* cu;                            // packed sequences, as in AttnFwdParams (or null)
   int nseq, max_len;
 };
@@ -220,6 +222,7 @@ struct DecodeProjParams {
   bf16_bits* sig;                           // (B, HN)
   int B, C, H, t_max;
   float eps, qscale;
+  float inv_n;  // 1 / head dimensions in use (head RMSNorm mean)
 };
 hipError_t launch_decode_proj_epilogue(const DecodeProjParams& p, int N, hipStream_t s);
 hipError_t launch_kv_append(const DecodeParams& p, int N, hipStream_t s);

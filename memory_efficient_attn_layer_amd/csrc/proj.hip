@@ -237,7 +237,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
 
     // Row coordinates. A tile inside one sequence (the usual case: T a
     // multiple of 128) needs no per-row division or bounds checks.
-    const float inv_c = 1.0f / (float)C, inv_n = 1.0f / (float)N, eps = p.eps;
+    const float inv_c = 1.0f / (float)C, inv_n = p.inv_n, eps = p.eps;
     // Everything below is instantiated twice: for a whole tile (one sequence,
     // inside M: no per-row division or bounds test) and for the rest.
     float nmax = 0.f;  // largest squared row norm of the wave's rotary projection

@@ -20,7 +20,11 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .attention import MAX_C_FORWARD, SUPPORTED_HEAD_DIMS, _validate
+from .attention import MAX_C_FORWARD, _validate
+
+# The cache holds whole heads: the zero-padded 16- and 32-wide heads of
+# fused_attn are not offered here.
+SUPPORTED_HEAD_DIMS = (64, 128)
 
 
 @dataclass
@@ -63,6 +67,8 @@ def prefill(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor
     H, N, eps = int(H), int(N), float(eps)
     weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
     _validate(x, weights, factor1, factor2, H, N, eps, False)
+    if N not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"the KV-cache path supports N in {SUPPORTED_HEAD_DIMS}, got N={N}")
     B, T, C = x.shape
     cache.check(B, H, N, x.device)
     Tc = cache.capacity
@@ -97,6 +103,8 @@ def decode_step(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, fa
     if x3.dim() != 3 or x3.shape[1] != 1:
         raise ValueError(f"x must be (B, C) or (B, 1, C), got {tuple(x.shape)}")
     _validate(x3, weights, factor1, factor2, H, N, eps, False)
+    if N not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"the KV-cache path supports N in {SUPPORTED_HEAD_DIMS}, got N={N}")
     B, _, C = x3.shape
     dev = x3.device
     cache.check(B, H, N, dev)

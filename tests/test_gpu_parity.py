@@ -116,6 +116,16 @@ BLOCK_CASES = [
     ("c64-h1-b2-t100", _w("c64", 2, 100, 64, 1, 64), None),
     ("c320-ne-hn-h2-n128-b1-t64", _w("c320", 1, 64, 320, 2, 128), None),
     ("c1344-h21-b1-t80", _w("c1344", 1, 80, 1344, 21, 64), None),
+    # Heads of 32 and 16 dimensions (carried zero-padded to 64; the head
+    # RMSNorm and the attention scale use the true width).
+    ("n32-h8-c256-b2-t100", _w("n32", 2, 100, 256, 8, 32), None),
+    ("n32-yarn4-h6-c192-b1-t300", _w("n32y", 1, 300, 192, 6, 32, 4.0, 128), None),
+    ("n16-h4-c64-b2-t70", _w("n16", 2, 70, 64, 4, 16), None),
+    # C = H*N a multiple of 32 only (odd H with N = 32, H = 2 with N = 16; a
+    # wide C whose last dx feature group holds 32 features).
+    ("n32-h3-c96-b2-t90", _w("n32h3", 2, 90, 96, 3, 32), None),
+    ("n16-h2-c32-b2-t64", _w("n16h2", 2, 64, 32, 2, 16), None),
+    ("n32-h33-c1056-b1-t50", _w("n32w", 1, 50, 1056, 33, 32), None),
 ]
 
 

@@ -51,8 +51,8 @@ def test_strerror_and_version(lib):
     assert lib.mea_version().decode().startswith("mea ")
 
 
-def _d(B=2, T=256, C=256, H=4, N=64, T_max=None, eps=1e-6):
-    return _lib.desc(B, T, C, H, N, T if T_max is None else T_max, eps)
+def _d(B=2, T=256, C=256, H=4, N=64, T_max=None, eps=1e-6, N_active=0):
+    return _lib.desc(B, T, C, H, N, T if T_max is None else T_max, eps, N_active)
 
 
 def test_workspace_bytes(lib):
@@ -82,8 +82,10 @@ def test_workspace_bytes(lib):
     "kw,code",
     [
         (dict(N=32), "MEA_ERR_HEAD_DIM"),
-        (dict(C=352), "MEA_ERR_MODEL_DIM"),
-        (dict(C=32), "MEA_ERR_MODEL_DIM"),
+        (dict(N_active=48), "MEA_ERR_HEAD_DIM"),
+        (dict(N=128, N_active=32), "MEA_ERR_HEAD_DIM"),
+        (dict(C=336), "MEA_ERR_MODEL_DIM"),
+        (dict(C=16), "MEA_ERR_MODEL_DIM"),
         (dict(T_max=100), "MEA_ERR_SHAPE"),
         (dict(H=0), "MEA_ERR_SHAPE"),
         (dict(eps=-1.0), "MEA_ERR_EPS"),
@@ -282,3 +284,42 @@ def test_static_decode_validation(lib):
     assert lib.mea_decode_static(ctypes.byref(big), *dargs, None) == _header_enum("MEA_ERR_SCRATCH")
     m = re.search(r"#define MEA_STATIC_SCRATCH_BYTES \((\d+)u << (\d+)\)", HEADER.read_text())
     assert int(m.group(1)) << int(m.group(2)) == _lib.MEA_STATIC_SCRATCH_BYTES
+
+
+def test_descriptor_accepts_padded_heads(lib):
+    """Heads of 16 or 32 dimensions are described as N = 64 with N_active."""
+    for n_act in (0, 16, 32, 64):
+        assert lib.mea_workspace_bytes(ctypes.byref(_d(N_active=n_act)), _lib.MEA_PASS_FWD) > 0
+    assert lib.mea_workspace_bytes(ctypes.byref(_d(N=128, N_active=128)), _lib.MEA_PASS_BWD) > 0
+
+
+def test_pad_heads_layout_and_gradients():
+    """The padding is differentiable and exact: every head keeps its N rows
+    (columns of Wo, table columns) in place, the padding is zero (identity
+    rotary pairs in the tables), and gradients of the padded tensors reach
+    the caller's tensors as their slices."""
+    from memory_efficient_attn_layer_amd.attention import PAD_N, _pad_heads
+
+    torch.manual_seed(0)
+    H, N, C, T = 3, 32, 96, 10
+    ws = [torch.randn(H * N, C, requires_grad=True) for _ in range(4)] + [torch.randn(C, H * N, requires_grad=True)]
+    f1 = torch.randn(T, N, requires_grad=True)
+    f2 = torch.randn(T, N, requires_grad=True)
+    (wq, wk, wv, wg, wo), p1, p2 = _pad_heads(H, N, ws, f1, f2)
+    assert wq.shape == (H * PAD_N, C) and wo.shape == (C, H * PAD_N) and p1.shape == (T, PAD_N)
+    for h in range(H):
+        assert torch.equal(wq[h * PAD_N:h * PAD_N + N], ws[0][h * N:(h + 1) * N])
+        assert torch.count_nonzero(wq[h * PAD_N + N:(h + 1) * PAD_N]) == 0
+        assert torch.equal(wo[:, h * PAD_N:h * PAD_N + N], ws[4][:, h * N:(h + 1) * N])
+        assert torch.count_nonzero(wo[:, h * PAD_N + N:(h + 1) * PAD_N]) == 0
+    assert torch.equal(p1[:, :N], f1) and torch.all(p1[:, N:] == 1)
+    assert torch.equal(p2[:, :N], f2) and torch.all(p2[:, N:] == 0)
+    gq = torch.randn_like(wq)
+    go = torch.randn_like(wo)
+    g1 = torch.randn_like(p1)
+    (wq * gq).sum().backward()
+    (wo * go).sum().backward()
+    (p1 * g1).sum().backward()
+    assert torch.equal(ws[0].grad, gq.reshape(H, PAD_N, C)[:, :N].reshape(H * N, C))
+    assert torch.equal(ws[4].grad, go.reshape(C, H, PAD_N)[:, :, :N].reshape(C, H * N))
+    assert torch.equal(f1.grad, g1[:, :N])
