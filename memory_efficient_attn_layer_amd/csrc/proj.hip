@@ -155,6 +155,10 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   if (nslab > 0) issue_next();
   if (nslab > 1) issue_next();
   int cmp_st = 0;  // stage of the slab being multiplied
+  // Largest squared row norm of the wave's rotary projection over all its
+  // tiles (wave wf holds q for wf = 0, k for wf = 1, in every rotary tile),
+  // published once after the last tile.
+  float nmax = 0.f;
   for (int ti = 0; ti < ntl; ++ti) {
     const ProjTile tl = proj_tile<N>(start + j0 + ti * nj, H);
 #pragma unroll
@@ -240,7 +244,6 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     const float inv_c = 1.0f / (float)C, inv_n = p.inv_n, eps = p.eps;
     // Everything below is instantiated twice: for a whole tile (one sequence,
     // inside M: no per-row division or bounds test) and for the rest.
-    float nmax = 0.f;  // largest squared row norm of the wave's rotary projection
     auto epilogue = [&](auto whole_tag) {
     constexpr bool whole = decltype(whole_tag)::value;
     int trow[TB], brow[TB];
@@ -400,16 +403,15 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       epilogue(std::true_type{});
     else
       epilogue(std::false_type{});
-    const int pjr = N == 64 ? wf : (tl.f0 == 0 ? 0 : 2) + wf;  // the rotary projection, if any
-    if (p.qk_norm2 != nullptr && pjr < 2) {
-      float v = nmax;
-      v = fmaxf(v, xor1(v));
-      v = fmaxf(v, xor2(v));
-      v = fmaxf(v, shfl_xor(v, 4));
-      v = fmaxf(v, shfl_xor(v, 8));
-      // Non-negative floats order like their bit patterns.
-      if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(p.qk_norm2) + pjr, __float_as_uint(v));
-    }
+  }
+  if (p.qk_norm2 != nullptr && ntl > 0) {
+    float v = nmax;
+    v = fmaxf(v, xor1(v));
+    v = fmaxf(v, xor2(v));
+    v = fmaxf(v, shfl_xor(v, 4));
+    v = fmaxf(v, shfl_xor(v, 8));
+    // Non-negative floats order like their bit patterns.
+    if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(p.qk_norm2) + wf, __float_as_uint(v));
   }
 }
 
