@@ -31,7 +31,7 @@ import torch
 
 from . import _lib
 
-SUPPORTED_HEAD_DIMS = (16, 32, 64, 128)
+SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 PADDED_HEAD_DIMS = (16, 32)  # carried zero-padded to PAD_N dimensions
 PAD_N = 64
 MAX_C_FORWARD = 4096

@@ -116,7 +116,8 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
         dot += xor1(dot);
         dot += xor2(dot);
         dot += shfl_xor(dot, 4);
-        if (CPR == 16) dot += shfl_xor(dot, 8);
+        if (CPR >= 16) dot += shfl_xor(dot, 8);
+        if (CPR == 32) dot += shfl_xor(dot, 16);
         const float rr = rrw[k];
         const float sc = rxv * rr, cf = dot * p.inv_n;
 #pragma unroll
@@ -176,7 +177,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // (two blocks sharing every K/V fragment) held two per SIMD ran 4.4% slower.
 // ---------------------------------------------------------------------------
 template <int N, bool VARLEN, bool TG>
-__global__ __launch_bounds__(256, N == 64 && !TG ? 3 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(256, N == 64 && !TG ? 3 : N == 256 ? 1 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   constexpr int QW = 32;                 // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
   constexpr int BQ = 4 * QW;             // queries per workgroup
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : 1) void attn_bwd_dkdv
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
   static_assert(KB == 1, "one 32-key block per wave");
   constexpr int BKV = 4 * KW;            // keys per workgroup
-  constexpr int BQ = 64;                 // queries per LDS tile
+  constexpr int BQ = N == 256 ? 32 : 64;  // queries per LDS tile (N = 256: 32, so Q, dO and V^T fit LDS)
   constexpr int CH = N / 8, KS = N / 16, DB = N / 32;
   constexpr int TILE = BQ * N;
   constexpr int LOADS = TILE / 8 / 256;
@@ -621,7 +622,7 @@ __global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : 1) void attn_bwd_dkdv
         }
       };
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
+      for (int sub = 0; sub < BQ / 32; ++sub) {
         const int qs0 = q0 + 32 * sub;
         if (qs0 + 31 < kw0 || qs0 >= T) continue;  // wave-uniform: nothing to add
         Sub u;
@@ -687,7 +688,7 @@ static hipError_t launch_bwd_variant(const AttnBwdParams& p, int N, int blocks_p
   // every head of its (sequence, block).
   const int G = (var ? p.nseq : p.B) * (tg ? 1 : p.H) * blocks_per_seq;
   if (G <= 0) return hipSuccess;
-  const int v = (N == 128 ? 4 : 0) | (var ? 2 : 0) | (tg ? 1 : 0);
+  const int v = (N == 128 ? 4 : N == 256 ? 8 : 0) | (var ? 2 : 0) | (tg ? 1 : 0);
   switch (v) {
     case 0: K<64, false, false>::launch(p, G, s); break;
     case 1: K<64, false, true>::launch(p, G, s); break;
@@ -696,7 +697,11 @@ static hipError_t launch_bwd_variant(const AttnBwdParams& p, int N, int blocks_p
     case 4: K<128, false, false>::launch(p, G, s); break;
     case 5: K<128, false, true>::launch(p, G, s); break;
     case 6: K<128, true, false>::launch(p, G, s); break;
-    default: K<128, true, true>::launch(p, G, s); break;
+    case 7: K<128, true, true>::launch(p, G, s); break;
+    case 8: K<256, false, false>::launch(p, G, s); break;
+    case 9: K<256, false, true>::launch(p, G, s); break;
+    case 10: K<256, true, false>::launch(p, G, s); break;
+    default: K<256, true, true>::launch(p, G, s); break;
   }
   return hipGetLastError();
 }

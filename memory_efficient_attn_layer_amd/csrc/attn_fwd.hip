@@ -46,7 +46,7 @@ namespace mea {
 // (sequence, h, query block) and every row index is taken relative to the
 // sequence's first token.
 template <int N, bool VARLEN>
-__global__ __launch_bounds__(256, N == 64 ? 4 : 2) void attn_fwd_kernel(AttnFwdParams p) {
+__global__ __launch_bounds__(256, N == 64 ? 4 : N == 128 ? 2 : 1) void attn_fwd_kernel(AttnFwdParams p) {
   constexpr int QW = 32;  // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
   constexpr int BQ = 4 * QW;             // queries per workgroup
@@ -350,10 +350,14 @@ hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s) {
     hipLaunchKernelGGL((attn_fwd_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
   else if (N == 64)
     hipLaunchKernelGGL((attn_fwd_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
-  else if (!var)
+  else if (N == 128 && !var)
     hipLaunchKernelGGL((attn_fwd_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
-  else
+  else if (N == 128)
     hipLaunchKernelGGL((attn_fwd_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
+  else if (!var)
+    hipLaunchKernelGGL((attn_fwd_kernel<256, false>), dim3(G), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<256, true>), dim3(G), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -224,10 +224,13 @@ __device__ __forceinline__ u32x4 stat_sel_b(bool on) {
 //    pairs) or bits 2-3 (16-chunk rows, over rows) must then take each value
 //    equally often, so the 4-chunk groups of the rows spread over the whole
 //    bank line instead of stacking on one quarter of it.
-// p ^ ((p & 1) << 2) and r ^ ((r & 3) << 2) satisfy both.
+// p ^ ((p & 1) << 2) and r ^ ((r & 3) << 2) satisfy both. Rows of 32 chunks
+// (256 bf16) take the 16-chunk swizzle: it permutes the low four bits of the
+// slot, so 16 consecutive rows still fill 16 distinct bank groups.
+// Every swizzle depends on row & 15 only.
 template <int CH>
 __device__ __forceinline__ int chunk_swz(int row) {
-  static_assert(CH == 8 || CH == 16, "rows of 64 or 128 bf16");
+  static_assert(CH == 8 || CH == 16 || CH == 32, "rows of 64, 128 or 256 bf16");
   if (CH == 8) {
     const int p = (row >> 1) & 7;
     return p ^ ((p & 1) << 2);

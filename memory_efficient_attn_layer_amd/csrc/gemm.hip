@@ -86,7 +86,7 @@ hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s) {
 // dZ block per 16 tokens and walks it as rows: lane (row, 8-feature chunk)
 // loads sig and O, writes dO into the head-major (B, H, T, N) layout, da_g,
 // z = O * sig over sig, and delta = rowsum(dO * O) per (token, head), summed
-// over the N / 8 lanes of the head.
+// over the N / 8 lanes of the head (N = 256: over the two waves of the head).
 // ---------------------------------------------------------------------------
 template <int NF>
 __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzParams p) {
@@ -94,6 +94,7 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzPara
   constexpr int FP = 128 + 4;  // fp32 staging pitch
   constexpr int SM_BYTES = S::SMEM * 2 > S::NW * 16 * FP * 4 ? S::SMEM * 2 : S::NW * 16 * FP * 4;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM_BYTES];
+  __shared__ float dpart[S::WF][S::BT];  // N = 256: each wave's half of delta
   const int M = p.M, C = p.C, H = p.H, T = p.T, N = p.N, HN = H * N;
   const int m0 = xcd_remap(blockIdx.x, gridDim.x) * S::BT, f0 = blockIdx.y * NF;
   f32x4 acc[8][4];
@@ -156,7 +157,16 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzPara
       dl += xor1(dl);
       dl += xor2(dl);
       dl += shfl_xor(dl, 4);
-      if (N == 128) dl += shfl_xor(dl, 8);
+      if (N >= 128) dl += shfl_xor(dl, 8);
+      if (N == 256) {
+        // A 256-wide head spans waves wf and wf ^ 1 (heads align to the
+        // 256-feature groups): add the other wave's half. N is uniform, and
+        // every (block, row) has its own slot.
+        const int tl = wt * 64 + tb * 16 + row;
+        if (cc == 0) dpart[wf][tl] = dl;
+        __syncthreads();
+        dl += dpart[wf ^ 1][tl];
+      }
       if (valid) {
         const int hh = jc / N, n = jc - hh * N;
         const int b = mc / T, t = mc - b * T;
@@ -178,7 +188,7 @@ static void launch_dz_nf(const DzParams& p, int HN, hipStream_t s) {
 
 hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s) {
   const int HN = p.H * p.N;
-  if (p.C % 32 != 0 || (p.N != 64 && p.N != 128)) return hipErrorInvalidValue;
+  if (p.C % 32 != 0 || (p.N != 64 && p.N != 128 && p.N != 256)) return hipErrorInvalidValue;
   // Feature groups of 512 where HN allows (see launch_gate_oproj).
   if (HN == 768)
     launch_dz_nf<768>(p, HN, s);

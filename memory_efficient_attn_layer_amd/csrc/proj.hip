@@ -65,12 +65,18 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   constexpr int FB = 8;                // 16-feature blocks per wave (128 features)
   constexpr int TB = BT / WT / 16;     // 16-token blocks per wave (4)
   constexpr int GB = TB / WF;          // Gram blocks per wave
-  constexpr int NPW = 128 / N;         // projections per wave
-  constexpr int GF = N / 16;           // feature blocks per projection
+  // N = 256 (HALF): a tile is one projection of one head and each wave holds
+  // half of it (128 of its 256 features); the head RMSNorm and the row norms
+  // then add the two waves' halves through LDS.
+  constexpr bool HALF = N == 256;
+  constexpr int NW128 = N < 128 ? N : 128;  // features of one projection in one wave
+  constexpr int NPW = 128 / NW128;     // projections per wave
+  constexpr int GF = NW128 / 16;       // feature blocks per projection in one wave
   constexpr int NSEG = BF / N;         // projections per stacked-weight slab
   constexpr int LOADS = (BF + BT) * BK / 8 / 64 / 4;  // load instructions per wave per slab
   __shared__ __attribute__((aligned(16))) bf16_bits smem[NS * STAGE];
   __shared__ float ssq_s[BT];
+  __shared__ float xch[HALF ? 2 : 1][HALF ? 2 : 1][HALF ? BT : 1];  // [ss | norm][wf][token] (HALF)
 
   // Locals, not captures of the argument block: a lambda holding &p would
   // force the block into scratch memory.
@@ -120,6 +126,9 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       wseg[NSEG > 1 ? 1 : 0] = wv;
       wseg[NSEG > 2 ? 2 : 0] = wk;
       wseg[NSEG > 3 ? 3 : 0] = wg;
+    } else if (NSEG == 1) {
+      // One projection per tile: q, k, v, g for f0 = 0, N, 2N, 3N.
+      wseg[0] = tl.f0 == 0 ? wq : tl.f0 == N ? wk : tl.f0 == 2 * N ? wv : wg;
     } else {
       wseg[0] = tl.f0 == 0 ? wq : wv;
       wseg[NSEG > 1 ? 1 : 0] = tl.f0 == 0 ? wk : wg;
@@ -156,9 +165,10 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   if (nslab > 1) issue_next();
   int cmp_st = 0;  // stage of the slab being multiplied
   // Largest squared row norm of the wave's rotary projection over all its
-  // tiles (wave wf holds q for wf = 0, k for wf = 1, in every rotary tile),
+  // tiles (wave wf holds q for wf = 0, k for wf = 1, in every rotary tile;
+  // with N = 256 every wave sees whole q and k rows: nmax for q, nmax_k for k),
   // published once after the last tile.
-  float nmax = 0.f;
+  float nmax = 0.f, nmax_k = 0.f;
   for (int ti = 0; ti < ntl; ++ti) {
     const ProjTile tl = proj_tile<N>(start + j0 + ti * nj, H);
 #pragma unroll
@@ -205,7 +215,8 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     const int m0 = tl.m0, h = tl.h;
     const int b0 = m0 / T, t0 = m0 - b0 * T;
     const bool tile_whole = m0 + BT <= M && t0 + BT <= T;
-    const bool has_rot = N == 64 || tl.f0 == 0;  // the wave holds q or k
+    const bool has_rot = N == 64 || (N == 128 ? tl.f0 == 0 : tl.f0 < 2 * N);  // the wave holds q or k
+    const int col = HALF ? wf * 128 : 0;  // first head column of the wave's features
     auto tab_row = [&](int tb) {
       const int m = m0 + wt * (TB * 16) + tb * 16 + c16;
       if (POS) return min(max(p.tpos[min(m, M - 1)], 0), p.t_max - 1);
@@ -218,7 +229,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     constexpr bool PREF = N == 64;
     f32x4 tab1[PREF ? GF : 1], tab2[PREF ? GF : 1];
     auto tab_at = [&](const float* f, int tb, int j) {
-      return *reinterpret_cast<const f32x4*>(f + (size_t)tab_row(tb) * N + 16 * j + 4 * g);
+      return *reinterpret_cast<const f32x4*>(f + (size_t)tab_row(tb) * N + col + 16 * j + 4 * g);
     };
     auto load_tab_j = [&](int tb, int j) {
       if (PREF) {
@@ -275,14 +286,16 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     // Each wave owns a 16-token x (NPW * N) block of it, rows of N + 8
     // elements, filled with 8-byte writes from the accumulator layout and
     // drained as 16-byte row chunks, so every store covers whole rows.
-    constexpr int SP = N + 8;
+    constexpr int SP = NW128 + 8;
     bf16_bits* stg = smem + ((ti * nk + nk - 1) % NS) * STAGE + wave * (NPW * 16 * SP);
     // Projection (0 q, 1 k, 2 v, 3 g) of the wave's gi-th N-feature block,
     // wave-uniform. For N = 64 the stacked rows are [q; v; k; g], so every
     // wave owns one rotary projection and one plain one and the epilogue work
     // is the same in all four waves; for N = 128 a tile is (q, k) or (v, g).
-    auto proj_of = [&](int gi) { return N == 64 ? (gi == 0 ? wf : 2 + wf) : (tl.f0 == 0 ? 0 : 2) + wf; };
-    constexpr int CPR = N / 8;               // 16-byte chunks per output row
+    auto proj_of = [&](int gi) {
+      return N == 64 ? (gi == 0 ? wf : 2 + wf) : N == 128 ? (tl.f0 == 0 ? 0 : 2) + wf : tl.f0 / N;
+    };
+    constexpr int CPR = NW128 / 8;           // 16-byte chunks per staged row
     // Drains the staged block of projection gi for token block tb into
     // dstp + b * bstride + t * tstride.
     // The lane index the store addresses derive from, opaque to the compiler
@@ -325,9 +338,17 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
         for (int r = 0; r < 4; ++r) ss += acc[gi * GF + j][tb][r] * acc[gi * GF + j][tb][r];
       ss += shfl_xor(ss, 16);
       ss += shfl_xor(ss, 32);
+      const int tlr = wt * (TB * 16) + tb * 16 + c16;
+      if (HALF) {
+        // Add the other wave's half of the row (every wave of the workgroup
+        // runs the same blocks, so the barrier is uniform).
+        if (g == 0) xch[0][HALF ? wf : 0][HALF ? tlr : 0] = ss;
+        __syncthreads();
+        ss += xch[0][HALF ? wf ^ 1 : 0][HALF ? tlr : 0];
+      }
       const float rr = rsqrtf(rx[tb] * rx[tb] * ss * inv_n + eps);
       const float sc = rx[tb] * rr * (pj == 0 ? p.qscale : 1.0f);  // folded into the table rows
-      if (ok[tb] && g == 0) {
+      if (ok[tb] && g == 0 && (!HALF || wf == 0)) {
         float* rstat = pj == 0 ? p.rq : p.rk;
         if (rstat != nullptr) rstat[((size_t)brow[tb] * H + h) * T + t] = rr;
       }
@@ -349,7 +370,17 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       }
       nrm += shfl_xor(nrm, 16);
       nrm += shfl_xor(nrm, 32);
-      nmax = fmaxf(nmax, nrm);
+      if (HALF) {
+        if (g == 0) xch[1][HALF ? wf : 0][HALF ? tlr : 0] = nrm;
+        __syncthreads();
+        nrm += xch[1][HALF ? wf ^ 1 : 0][HALF ? tlr : 0];
+        if (pj == 0)
+          nmax = fmaxf(nmax, nrm);
+        else
+          nmax_k = fmaxf(nmax_k, nrm);
+      } else {
+        nmax = fmaxf(nmax, nrm);
+      }
     };
     // v = rx acc; g = sigmoid(rx acc) = 1 / (1 + exp2(-log2(e) rx acc)).
     auto plain_block = [&](int tb, int gi) {
@@ -368,11 +399,11 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     auto drain_pj = [&](int gi, int tb) {
       const int pj = proj_of(gi);
       if (pj < 2)
-        drain(gi, tb, (pj == 0 ? p.q : p.k) + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
+        drain(gi, tb, (pj == 0 ? p.q : p.k) + (size_t)h * T * N + col, (size_t)H * T * N, (size_t)N);
       else if (pj == 2)
-        drain(gi, tb, p.v + (size_t)h * T * N, (size_t)H * T * N, (size_t)N);
+        drain(gi, tb, p.v + (size_t)h * T * N + col, (size_t)H * T * N, (size_t)N);
       else
-        drain(gi, tb, p.sig + (size_t)h * N, (size_t)T * HN, (size_t)HN);
+        drain(gi, tb, p.sig + (size_t)h * N + col, (size_t)T * HN, (size_t)HN);
     };
     if (N == 64) {
       // The plain projection (v or g) of every block first, while the table
@@ -405,13 +436,20 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       epilogue(std::false_type{});
   }
   if (p.qk_norm2 != nullptr && ntl > 0) {
-    float v = nmax;
-    v = fmaxf(v, xor1(v));
-    v = fmaxf(v, xor2(v));
-    v = fmaxf(v, shfl_xor(v, 4));
-    v = fmaxf(v, shfl_xor(v, 8));
-    // Non-negative floats order like their bit patterns.
-    if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(p.qk_norm2) + wf, __float_as_uint(v));
+    auto publish = [&](float v, int slot) {
+      v = fmaxf(v, xor1(v));
+      v = fmaxf(v, xor2(v));
+      v = fmaxf(v, shfl_xor(v, 4));
+      v = fmaxf(v, shfl_xor(v, 8));
+      // Non-negative floats order like their bit patterns.
+      if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(p.qk_norm2) + slot, __float_as_uint(v));
+    };
+    if (HALF) {
+      publish(nmax, 0);
+      publish(nmax_k, 1);
+    } else {
+      publish(nmax, wf);
+    }
   }
 }
 
@@ -435,10 +473,14 @@ hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s) {
     hipLaunchKernelGGL((qkvg_proj_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
   else if (N == 64)
     hipLaunchKernelGGL((qkvg_proj_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
-  else if (!pos)
+  else if (N == 128 && !pos)
     hipLaunchKernelGGL((qkvg_proj_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
-  else
+  else if (N == 128)
     hipLaunchKernelGGL((qkvg_proj_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
+  else if (!pos)
+    hipLaunchKernelGGL((qkvg_proj_kernel<256, false>), dim3(G), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((qkvg_proj_kernel<256, true>), dim3(G), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -126,6 +126,12 @@ BLOCK_CASES = [
     ("n32-h3-c96-b2-t90", _w("n32h3", 2, 90, 96, 3, 32), None),
     ("n16-h2-c32-b2-t64", _w("n16h2", 2, 64, 32, 2, 16), None),
     ("n32-h33-c1056-b1-t50", _w("n32w", 1, 50, 1056, 33, 32), None),
+    # Heads of 256 dimensions: one wave per SIMD in the attention kernels,
+    # 32-query tiles in dK/dV, the projection's and dZ's head sums over two
+    # waves.
+    ("n256-h2-c512-b2-t130", _w("n256", 2, 130, 512, 2, 256), None),
+    ("n256-yarn4-h3-c768-b1-t200", _w("n256y", 1, 200, 768, 3, 256, 4.0, 64), None),
+    ("n256-h1-c256-b1-t70", _w("n256h1", 1, 70, 256, 1, 256), None),
 ]
 
 

@@ -69,8 +69,9 @@ def _oracle(inp, lens, H, N):
 
 @pytest.mark.parametrize(
     "lens,C,H,N",
-    [([77, 256, 300, 1, 513], 256, 2, 64), ([130, 64, 200], 512, 4, 128)],
-    ids=["n64-5seq", "n128-3seq"],
+    [([77, 256, 300, 1, 513], 256, 2, 64), ([130, 64, 200], 512, 4, 128), ([90, 33, 160], 512, 2, 256),
+     ([70, 130], 96, 3, 32)],
+    ids=["n64-5seq", "n128-3seq", "n256-3seq", "n32-2seq"],
 )
 def test_varlen_forward_backward_matches_oracle_per_sequence(lens, C, H, N):
     inp = _inputs(lens, C, H, N, t_max=max(lens) + 40, seed=21)
