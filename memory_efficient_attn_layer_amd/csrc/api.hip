@@ -620,7 +620,6 @@ int mea_prefill(const mea_desc* d, const void* x, const void* wq, const void* wk
                 int64_t cache_T, void* ws, size_t ws_bytes, void* stream) {
   int rc = validate(d, MEA_PASS_FWD);
   if (rc != MEA_OK) return rc;
-  if (d->N == 256) return MEA_ERR_HEAD_DIM;  // the KV-cache calls hold heads of 64 or 128
   rc = check_ptrs({k_cache, v_cache});
   if (rc != MEA_OK) return rc;
   if (cache_T < d->T || cache_T > d->T_max) return MEA_ERR_SHAPE;
@@ -685,7 +684,6 @@ int decode_check(const mea_desc* d, const void* x, const void* wq, const void* w
                  void* y) {
   int rc = validate(d, MEA_PASS_FWD);
   if (rc != MEA_OK) return rc;
-  if (d->N == 256) return MEA_ERR_HEAD_DIM;  // the KV-cache calls hold heads of 64 or 128
   rc = check_ptrs({x, wq, wk, wv, wg, wo, f1, f2, k_cache, v_cache, y});
   if (rc != MEA_OK) return rc;
   if (pos == nullptr) return MEA_ERR_NULL;
@@ -839,7 +837,7 @@ const char* mea_strerror(int code) {
     case MEA_OK: return "ok";
     case MEA_ERR_NULL: return "a required pointer is NULL (or only one of a pair was given)";
     case MEA_ERR_SHAPE: return "B, T, H must be >= 1, T <= T_max, and indices must fit 31 bits";
-    case MEA_ERR_HEAD_DIM: return "head width N must be 64, 128 or 256 (64 or 128 for the KV-cache calls)";
+    case MEA_ERR_HEAD_DIM: return "head width N must be 64, 128 or 256";
     case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 32 in [32, 4096]";
     case MEA_ERR_WORKSPACE: return "workspace smaller than mea_workspace_bytes()";
     case MEA_ERR_ALIGN: return "a pointer is not 16-byte aligned";

@@ -252,7 +252,8 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyParams p) {
   }
 }
 
-// Sum over the N threads of a workgroup (N = 64 or 128); every thread gets it.
+// Sum over the N threads of a workgroup (N = 64, 128 or 256: N / 64 waves,
+// added in wave order); every thread gets it.
 template <int N>
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
@@ -261,7 +262,10 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   __syncthreads();  // earlier readers of red are done
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return red[0] + red[1];
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < N / 64; ++w) t += red[w];
+  return t;
 }
 
 // One workgroup of N threads per (b, h); thread n owns feature n of the head.
@@ -271,7 +275,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // pos[b], q times qscale, v plain, sigmoid(g) (:123).
 template <int N>
 __global__ __launch_bounds__(N) void decode_proj_epilogue_kernel(DecodeProjParams p) {
-  __shared__ float red[2];
+  __shared__ float red[N / 64 > 1 ? N / 64 : 1];
   const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H, n = threadIdx.x;
   const int HN = p.H * N;
   float ss = 0.f;
@@ -312,6 +316,8 @@ hipError_t launch_decode_proj_epilogue(const DecodeProjParams& p, int N, hipStre
     hipLaunchKernelGGL(decode_proj_epilogue_kernel<64>, dim3(p.B * p.H), dim3(64), 0, s, p);
   else if (N == 128)
     hipLaunchKernelGGL(decode_proj_epilogue_kernel<128>, dim3(p.B * p.H), dim3(128), 0, s, p);
+  else if (N == 256)
+    hipLaunchKernelGGL(decode_proj_epilogue_kernel<256>, dim3(p.B * p.H), dim3(256), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -343,6 +349,8 @@ hipError_t launch_attn_decode(const DecodeParams& p, int N, hipStream_t s) {
     hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(64 * kDecodeWaves), 0, s, p);
   else if (N == 128)
     hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(64 * kDecodeWaves), 0, s, p);
+  else if (N == 256)
+    hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(64 * kDecodeWaves), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -353,6 +361,8 @@ hipError_t launch_attn_decode_combine(const DecodeParams& p, int N, hipStream_t 
     hipLaunchKernelGGL(attn_decode_combine_kernel<64>, dim3(p.B * p.H), dim3(256), 0, s, p);
   else if (N == 128)
     hipLaunchKernelGGL(attn_decode_combine_kernel<128>, dim3(p.B * p.H), dim3(256), 0, s, p);
+  else if (N == 256)
+    hipLaunchKernelGGL(attn_decode_combine_kernel<256>, dim3(p.B * p.H), dim3(256), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -20,23 +20,26 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .attention import MAX_C_FORWARD, _validate
+from .attention import MAX_C_FORWARD, PAD_N, PADDED_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _pad_heads, _validate
 
-# The cache holds whole heads: the zero-padded 16- and 32-wide heads of
-# fused_attn are not offered here.
-SUPPORTED_HEAD_DIMS = (64, 128)
+
+def cache_width(N: int) -> int:
+    """Width of a cache row for heads of N dimensions: heads of 16 or 32
+    dimensions are carried zero-padded to PAD_N, as in fused_attn."""
+    return PAD_N if N in PADDED_HEAD_DIMS else N
 
 
 @dataclass
 class KVCache:
-    """Per-layer cache: ``k`` and ``v`` of shape (B, H, capacity, N), bf16."""
+    """Per-layer cache: ``k`` and ``v`` of shape (B, H, capacity, cache_width(N)),
+    bf16 (heads of 16 or 32 dimensions as zero-padded rows of 64)."""
 
     k: torch.Tensor
     v: torch.Tensor
 
     @classmethod
     def empty(cls, B: int, H: int, N: int, capacity: int, device) -> "KVCache":
-        shape = (B, H, capacity, N)
+        shape = (B, H, capacity, cache_width(N))
         return cls(torch.zeros(shape, device=device, dtype=torch.bfloat16),
                    torch.zeros(shape, device=device, dtype=torch.bfloat16))
 
@@ -45,13 +48,24 @@ class KVCache:
         return self.k.shape[2]
 
     def check(self, B: int, H: int, N: int, device) -> None:
+        W = cache_width(N)
         for name, t in (("k", self.k), ("v", self.v)):
-            if tuple(t.shape) != (B, H, self.capacity, N):
-                raise ValueError(f"cache.{name} has shape {tuple(t.shape)}, expected {(B, H, self.capacity, N)}")
+            if tuple(t.shape) != (B, H, self.capacity, W):
+                raise ValueError(f"cache.{name} has shape {tuple(t.shape)}, expected {(B, H, self.capacity, W)}")
             if t.dtype != torch.bfloat16 or not t.is_contiguous():
                 raise ValueError(f"cache.{name} must be a contiguous bfloat16 tensor")
             if t.device != device:
                 raise ValueError(f"cache.{name} is on {t.device}, x is on {device}")
+
+
+def _padded(H: int, N: int, weights, factor1, factor2):
+    """(weights, tables, N, N_active) as the library takes them: heads of 16
+    or 32 dimensions zero-padded to PAD_N (no gradient is taken here)."""
+    if N not in PADDED_HEAD_DIMS:
+        return weights, factor1, factor2, N, 0
+    with torch.no_grad():
+        w, f1, f2 = _pad_heads(H, N, weights, factor1, factor2)
+    return w, f1, f2, PAD_N, N
 
 
 def _tables(factor1, factor2, rows: int):
@@ -67,10 +81,9 @@ def prefill(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor
     H, N, eps = int(H), int(N), float(eps)
     weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
     _validate(x, weights, factor1, factor2, H, N, eps, False)
-    if N not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"the KV-cache path supports N in {SUPPORTED_HEAD_DIMS}, got N={N}")
     B, T, C = x.shape
     cache.check(B, H, N, x.device)
+    weights, factor1, factor2, N, n_active = _padded(H, N, weights, factor1, factor2)
     Tc = cache.capacity
     if Tc < T:
         raise ValueError(f"cache capacity {Tc} is smaller than the prompt length {T}")
@@ -79,7 +92,7 @@ def prefill(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor
     xc = x.contiguous()
     wc = [w.contiguous() for w in weights]
     f1, f2 = _tables(factor1, factor2, Tc)
-    d = _lib.desc(B, T, C, H, N, Tc, eps)
+    d = _lib.desc(B, T, C, H, N, Tc, eps, n_active)
     y = torch.empty((B, T, C), device=dev, dtype=torch.bfloat16)
     ws_bytes = lib.mea_workspace_bytes(d, _lib.MEA_PASS_FWD)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
@@ -103,11 +116,18 @@ def decode_step(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, fa
     if x3.dim() != 3 or x3.shape[1] != 1:
         raise ValueError(f"x must be (B, C) or (B, 1, C), got {tuple(x.shape)}")
     _validate(x3, weights, factor1, factor2, H, N, eps, False)
-    if N not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"the KV-cache path supports N in {SUPPORTED_HEAD_DIMS}, got N={N}")
     B, _, C = x3.shape
     dev = x3.device
     cache.check(B, H, N, dev)
+    weights, factor1, factor2, N, n_active = _padded(H, N, weights, factor1, factor2)
+    return _decode_launch(x3, weights, factor1, factor2, H, N, n_active, pos, cache, eps, squeeze)
+
+
+def _decode_launch(x3, weights, factor1, factor2, H, N, n_active, pos, cache, eps, squeeze):
+    """The library call of one decode step (weights and tables as the
+    library takes them, see _padded)."""
+    B, _, C = x3.shape
+    dev = x3.device
     Tc = cache.capacity
     if not isinstance(pos, torch.Tensor):
         pos = torch.tensor(list(pos), dtype=torch.int32, device=dev)
@@ -118,7 +138,7 @@ def decode_step(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, fa
     wc = [w.contiguous() for w in weights]
     posc = pos.contiguous()
     f1, f2 = _tables(factor1, factor2, Tc)
-    d = _lib.desc(B, Tc, C, H, N, Tc, eps)
+    d = _lib.desc(B, Tc, C, H, N, Tc, eps, n_active)
     y = torch.empty((B, 1, C), device=dev, dtype=torch.bfloat16)
     ws_bytes = lib.mea_decode_workspace_bytes(d)
     if ws_bytes == 0:
@@ -149,9 +169,16 @@ class DecodeGraph:
                  cache: KVCache, eps: float = 1e-6, warmup: int = 2):
         B, dev = cache.k.shape[0], cache.k.device
         C = q_weight.shape[1]
-        self._w = [w.contiguous() for w in (q_weight, k_weight, v_weight, g_weight, o_weight)]
+        H, N = int(H), int(N)
+        weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
+        _validate(torch.empty((B, 1, C), device=dev, dtype=torch.bfloat16), weights, factor1, factor2, H, N,
+                  float(eps), False)
+        cache.check(B, H, N, dev)
+        # Padded once here, so the captured step allocates nothing.
+        weights, factor1, factor2, Nl, n_active = _padded(H, N, weights, factor1, factor2)
+        self._w = [w.contiguous() for w in weights]
         self._f1, self._f2 = _tables(factor1, factor2, cache.capacity)
-        self._args = (H, N)
+        self._args = (H, Nl, n_active)
         self._cache, self._eps = cache, float(eps)
         self.x = torch.zeros((B, C), device=dev, dtype=torch.bfloat16)
         self.pos = torch.zeros((B,), device=dev, dtype=torch.int32)
@@ -170,7 +197,9 @@ class DecodeGraph:
             self.y = self._run(self._cache)
 
     def _run(self, cache: KVCache):
-        return decode_step(self.x, *self._w, self._f1, self._f2, *self._args, self.pos, cache, self._eps)
+        H, Nl, n_active = self._args
+        return _decode_launch(self.x.unsqueeze(1), self._w, self._f1, self._f2, H, Nl, n_active, self.pos, cache,
+                              self._eps, True)
 
     def step(self, x, pos) -> torch.Tensor:
         self.x.copy_(x)
@@ -179,4 +208,4 @@ class DecodeGraph:
         return self.y
 
 
-__all__ = ["KVCache", "DecodeGraph", "prefill", "decode_step", "SUPPORTED_HEAD_DIMS", "MAX_C_FORWARD"]
+__all__ = ["KVCache", "DecodeGraph", "prefill", "decode_step", "cache_width", "SUPPORTED_HEAD_DIMS", "MAX_C_FORWARD"]

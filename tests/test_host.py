@@ -280,9 +280,8 @@ def test_static_decode_validation(lib):
     no_pos[8] = None
     assert lib.mea_decode_static(ctypes.byref(d), *no_pos, None) == _header_enum("MEA_ERR_NULL")
     assert lib.mea_decode_static(ctypes.byref(_d(N=96)), *dargs, None) == _header_enum("MEA_ERR_HEAD_DIM")
-    # Heads of 256 dimensions run in the training entry points, not in the KV-cache calls.
-    assert lib.mea_decode_static(ctypes.byref(_d(N=256, C=512, H=2)), *dargs, None) == _header_enum("MEA_ERR_HEAD_DIM")
     assert lib.mea_workspace_bytes(ctypes.byref(_d(N=256, C=512, H=2)), _lib.MEA_PASS_BWD) > 0
+    assert lib.mea_decode_workspace_bytes(ctypes.byref(_d(N=256, C=512, H=2))) > 0
     big = _d(B=4096, T=512, T_max=512, C=2048, H=16, N=128)
     assert lib.mea_decode_workspace_bytes(ctypes.byref(big)) > _lib.MEA_STATIC_SCRATCH_BYTES
     assert lib.mea_decode_static(ctypes.byref(big), *dargs, None) == _header_enum("MEA_ERR_SCRATCH")
