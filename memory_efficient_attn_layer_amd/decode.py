@@ -5,7 +5,8 @@ The reference trains only and has no decode path; these run the same block
 math (README.md:42-64) through ``mea_prefill`` / ``mea_decode`` of libmea.so.
 The cache holds, per (batch, head), the k rows exactly as the attention uses
 them (RMS-normalised over N and rotated) and the plain v rows, bf16, in a
-``(B, H, capacity, N)`` layout. Sequence b's new token sits at position
+``(B, H, capacity, cache_width(N))`` layout (heads of 16 or 32 dimensions are
+held zero-padded to 64). Sequence b's new token sits at position
 ``pos[b]``: it reads rotary row ``pos[b]``, its k / v are written to cache row
 ``pos[b]``, and it attends to rows ``0 .. pos[b]``, so sequences of a batch may
 have different lengths.
