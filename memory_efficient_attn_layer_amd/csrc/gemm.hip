@@ -330,6 +330,7 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
     for (int fb = 0; fb < FB; ++fb)
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = mfma(af[fb], bfr[tb], acc[fb][tb]);
+    reads_then_products<FB + TB, FB * TB>();
   }
 
   // Epilogue. The x block of each wave (its 64 tokens x 128 features, 16 KB)

@@ -206,6 +206,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
         for (int j = 1; j < WF; ++j) xb = wf == j ? bfr[j * GB + i] : xb;
         gram[i] = mfma(xb, xb, gram[i]);
       }
+      reads_then_products<FB + TB, FB * TB + GB>();
     }
 
     // Rotary table rows of the wave's tokens are fetched ahead of their use

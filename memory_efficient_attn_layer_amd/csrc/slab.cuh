@@ -91,6 +91,18 @@ __device__ __forceinline__ u32x4 slab_read(const bf16_bits* lds, int row, int ch
   return *reinterpret_cast<const u32x4*>(lds + row * KS + ((chunk ^ slab_swz<KS>(row)) << 3));
 }
 
+// Scheduling of one slab step of an MFMA main loop: the wave's NREAD LDS
+// fragment reads first, then its NMFMA products (placed after them in the
+// same basic block). Left to itself the scheduler keeps one or two fragments
+// in registers and waits for each read in turn, one LDS round trip per group
+// of four products; issued together the reads return while the first
+// products run, and the waits count down (lgkmcnt(n-1), ..., 0).
+template <int NREAD, int NMFMA>
+__device__ __forceinline__ void reads_then_products() {
+  __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);  // DS reads
+  __builtin_amdgcn_sched_group_barrier(0x008, NMFMA, 0);  // MFMA
+}
+
 // Sum of squares of 8 bf16 values (exact fp32 products, fp32 accumulation).
 __device__ __forceinline__ float sumsq8(const u32x4& v, float acc) {
 #pragma unroll

@@ -104,6 +104,7 @@ __device__ __forceinline__ void tok_mainloop(int K, bf16_bits* smem, const bf16_
     for (int fb = 0; fb < S::FB; ++fb)
 #pragma unroll
       for (int tb = 0; tb < S::TB; ++tb) acc[fb][tb] = mfma(af[fb], bfr[tb], acc[fb][tb]);
+    reads_then_products<S::FB + S::TB, S::FB * S::TB>();
   };
 
 #pragma unroll
