@@ -422,8 +422,8 @@ __global__ __launch_bounds__(256, N == 64 && !TG ? 3 : N == 256 ? 1 : 2) void at
 //   dV^T += dO^T P   and   dK^T += Q^T dS
 // whose A operands dO^T, Q^T are read from the same row-major LDS tiles with
 // the transposing ds_read_b64_tr_b16. Query tiles of 64 stream through LDS
-// (global_load_lds, double-buffered, one barrier per tile), starting at the
-// block's first key (causal). For N = 64 three workgroups share a CU (168
+// (global_load_lds, double-buffered, one barrier per tile), from the last
+// tile down to the one holding the block's first key (causal). For N = 64 three workgroups share a CU (168
 // registers, 50 KB of LDS each): the same work at two per CU, with V^T in
 // registers and two 32-query steps interleaved for instruction-level
 // parallelism, ran 7.4% slower. N = 128 runs one wave per SIMD, whose 512
@@ -551,14 +551,19 @@ __global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : 1) void attn_bwd_dkdv
     // query side is zero in the lanes holding k-elements 8..15).
     const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
 
+    // Query tiles are walked from the last one down: every workgroup of a
+    // head then reads the same tile at about the same time (walking up from
+    // each block's own diagonal, they read as many different tiles at once as
+    // there are key blocks), which cut this kernel's HBM reads from 2.74 to
+    // 2.27 GB per launch at B64 T4096 C512 H8 N64.
     const int nq = (T - k0 + BQ - 1) / BQ;
-    issue_tile(k0, 0);
+    issue_tile(k0 + (nq - 1) * BQ, 0);
     wait_vmcnt0();
     publish_stats(0);
     __syncthreads();
     for (int it = 0; it < nq; ++it) {
-      const int q0 = k0 + it * BQ;
-      if (it + 1 < nq) issue_tile(q0 + BQ, (it + 1) & 1);
+      const int q0 = k0 + (nq - 1 - it) * BQ;
+      if (it + 1 < nq) issue_tile(q0 - BQ, (it + 1) & 1);
       const bf16_bits* qt = tiles + (it & 1) * 2 * TILE;
       const bf16_bits* dt = qt + TILE;
       const u32x4* sts = stats + (it & 1) * (BQ + 1);

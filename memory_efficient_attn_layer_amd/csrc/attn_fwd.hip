@@ -192,6 +192,25 @@ __global__ __launch_bounds__(256, N == 64 ? 4 : N == 128 ? 2 : 1) void attn_fwd_
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + st * 32 * N + koff[ks]));
+    // N = 64: the V^T fragments of the step are read with the K fragments,
+    // before the S products, and the scheduling fence keeps them there (128
+    // registers, still four workgroups per CU): read next to the PV products
+    // that use them, each read's LDS round trip stalled the wave (the kernel
+    // ran 1.9% slower). N = 128 and 256 have no registers to spare and read
+    // them at the products.
+    constexpr bool VEARLY = N == 64;
+    auto vread = [&](int kst, int db) {
+      const bf16_bits* vr = vs_t + (st * 32 + 16 * kst) * N;
+      return frag_from2(lds_read_tr4(vr + voff[0][db]), lds_read_tr4(vr + voff[1][db]));
+    };
+    bf16x8 vfr[VEARLY ? 2 : 1][VEARLY ? DB : 1];
+    if constexpr (VEARLY) {
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) vfr[kst][db] = vread(kst, db);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     bf16x8 pf[QB][2];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -254,8 +273,7 @@ __global__ __launch_bounds__(256, N == 64 ? 4 : N == 128 ? 2 : 1) void attn_fwd_
     for (int kst = 0; kst < 2; ++kst) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const bf16_bits* vr = vs_t + (st * 32 + 16 * kst) * N;
-        const bf16x8 vf = frag_from2(lds_read_tr4(vr + voff[0][db]), lds_read_tr4(vr + voff[1][db]));
+        const bf16x8 vf = VEARLY ? vfr[VEARLY ? kst : 0][VEARLY ? db : 0] : vread(kst, db);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           if (MASK && kb0 > q0w + 32 * qb + 31) continue;
