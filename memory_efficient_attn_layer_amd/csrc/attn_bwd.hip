@@ -421,21 +421,26 @@ __global__ __launch_bounds__(256, N == 64 && !TG ? 3 : N == 256 ? 1 : 2) void at
 // lane, so P and dS = P (dP - delta) are already the B operands (k = query) of
 //   dV^T += dO^T P   and   dK^T += Q^T dS
 // whose A operands dO^T, Q^T are read from the same row-major LDS tiles with
-// the transposing ds_read_b64_tr_b16. Query tiles of 64 stream through LDS
-// (global_load_lds, double-buffered, one barrier per tile), from the last
-// tile down to the one holding the block's first key (causal). For N = 64 three workgroups share a CU (168
-// registers, 50 KB of LDS each): the same work at two per CU, with V^T in
-// registers and two 32-query steps interleaved for instruction-level
-// parallelism, ran 7.4% slower. N = 128 runs one wave per SIMD, whose 512
-// registers hold the operands without spilling.
+// the transposing ds_read_b64_tr_b16. Query tiles (64 queries for N = 64,
+// 32 for N >= 128) stream through LDS (global_load_lds, double-buffered, one
+// barrier per tile), from the last tile down to the one holding the block's
+// first key (causal). For N = 64 three workgroups share a CU (168 registers,
+// 50 KB of LDS each): the same work at two per CU, with V^T in registers and
+// two 32-query steps interleaved for instruction-level parallelism, ran 7.4%
+// slower. For N = 128 two workgroups share a CU (252 registers, 66 KB of LDS
+// each); with 64-query tiles (97 KB of LDS) only one fitted, one wave per
+// SIMD, and the kernel ran 36% longer. N = 256 (and N = 128 with table
+// gradients, whose extra state would spill at 256 registers) runs one wave
+// per SIMD.
 // ---------------------------------------------------------------------------
 template <int N, bool VARLEN, bool TG>
-__global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : N == 128 && !TG ? 2 : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
   constexpr int KW = 32;                 // keys per wave
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
   static_assert(KB == 1, "one 32-key block per wave");
   constexpr int BKV = 4 * KW;            // keys per workgroup
-  constexpr int BQ = N == 256 ? 32 : 64;  // queries per LDS tile (N = 256: 32, so Q, dO and V^T fit LDS)
+  constexpr int BQ = N >= 128 ? 32 : 64;  // queries per LDS tile (N >= 128: 32, so that Q, dO and V^T of two
+                                         // workgroups fit LDS at N = 128, and of one at N = 256)
   constexpr int CH = N / 8, KS = N / 16, DB = N / 32;
   constexpr int TILE = BQ * N;
   constexpr int LOADS = TILE / 8 / 256;
