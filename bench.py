@@ -12,7 +12,7 @@ the dominant kernel (timed live with HIP events on its launch stream over the
 timed region), peak HBM, and the CPU baseline (the fp32 oracle on a bounded
 batch slice on the host cores). Progress goes to stderr.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-eager] [--no-cpu-baseline] [--table-grad]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-eager] [--no-cpu-baseline] [--no-box-reference] [--table-grad]
     python bench.py --workload 2|3       # the same line for another fwd+bwd workload
     python bench.py --workload 4         # forward-only (prefill) workload: fwd tokens/s, no CPU leg
     python bench.py --workload W --varlen  # B packed sequences of seeded lengths in [T/4, T], fwd+bwd
@@ -165,6 +165,39 @@ def peak_of(step, sync):
     return torch.cuda.max_memory_allocated() - base
 
 
+def box_reference():
+    """Speed of this GPU on two vendor operations, for comparing runs made on
+    different machines: a bf16 matrix product of 8192^3 (torch.matmul of two
+    contiguous 2-D tensors) in TFLOP/s and a 1 GiB device-to-device copy in
+    GB/s (bytes read plus written). Measured outside the timed region."""
+    import torch
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) * 1e-3 / reps
+
+    n = 8192
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+    y = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+    gemm = 2 * n**3 / timed(lambda: torch.matmul(x, y), 10) / 1e12
+    del x, y
+    src = torch.empty(2**30, device="cuda", dtype=torch.uint8)
+    dst = torch.empty_like(src)
+    copy = 2 * 2**30 / timed(lambda: dst.copy_(src), 10) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"gemm_bf16_tflops": round(gemm, 1), "copy_gbs": round(copy, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -176,6 +209,8 @@ def main():
     ap.add_argument("--table-grad", action="store_true",
                     help="also differentiate the rotary tables (dF1 / dF2, as the reference always does)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-box-reference", action="store_true",
+                    help="skip the vendor GEMM / copy speed reference (keeps kernel traces to this library)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--varlen", action="store_true",
                     help="pack B sequences of seeded random lengths in [T/4, T] (fwd+bwd, packed-sequence path)")
@@ -306,6 +341,10 @@ def main():
         except Exception as e:  # noqa: BLE001 - report, do not fail the benchmark
             eager = {"error": f"{type(e).__name__}: {e}"[:300]}
 
+    box = None if args.no_box_reference else box_reference()
+    if box:
+        log(f"box reference: bf16 GEMM {box['gemm_bf16_tflops']} TFLOP/s, copy {box['copy_gbs']} GB/s")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline (fp32 oracle)")
@@ -334,6 +373,7 @@ def main():
         "roofline": roofline,
         "attention": attention,
         "kernels": kernels,
+        "box_reference": box,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -409,6 +449,7 @@ def forward_bench(args, w):
         "block_tflops": round(w.flops_fwd() / sec / 1e12, 2),
         "roofline": roofline_of(prof, work),
         "kernels": kernels,
+        "box_reference": None if args.no_box_reference else box_reference(),
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
@@ -491,6 +532,7 @@ def varlen_bench(args, w):
         "block_tflops": round(flops / sec / 1e12, 2),
         "roofline": roofline_of(prof, work),
         "kernels": kernels,
+        "box_reference": None if args.no_box_reference else box_reference(),
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
@@ -579,6 +621,7 @@ def decode_bench(args, w):
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": None},
         "kernels": kernels,
+        "box_reference": None if args.no_box_reference else box_reference(),
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
