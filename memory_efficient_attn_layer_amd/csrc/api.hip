@@ -136,12 +136,12 @@ T* at(void* ws, size_t off) {
 enum KernelId {
   K_QKVG_PROJ, K_ATTN_FWD, K_GATE_OPROJ, K_TRANSPOSE, K_ZERO, K_DZ_GATE_BWD,
   K_ATTN_BWD_DQ, K_ATTN_BWD_DKDV, K_DW_PARTIAL, K_DW_REDUCE, K_DX,
-  K_KV_APPEND, K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_REDUCE, K_COUNT
+  K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_REDUCE, K_COUNT
 };
 const char* const kKernelNames[K_COUNT] = {
     "qkvg_proj", "attn_fwd", "gate_oproj", "transpose", "zero_f32", "dz_gate_bwd",
     "attn_bwd_dq", "attn_bwd_dkdv", "dw_partial", "dw_reduce", "dx",
-    "kv_append", "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad_reduce"};
+    "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad_reduce"};
 
 struct ProfRec {
   int kernel;
@@ -641,10 +641,10 @@ int mea_prefill(const mea_desc* d, const void* x, const void* wq, const void* wk
 namespace {
 
 // Decode workspace: the raw products [a_q|a_k|a_v|a_g] (B x 4HN fp32), the
-// new token's q, k, v, sigmoid(g) and attention output (B x H*N bf16 each)
-// and the split partials.
+// new token's q, sigmoid(g) and attention output (B x H*N bf16 each; its k
+// and v go straight to the caches) and the split partials.
 struct DecLayout {
-  size_t a, q, k, v, sig, o, part, total;
+  size_t a, q, sig, o, part, total;
   int S, chunk;
 };
 
@@ -656,8 +656,6 @@ DecLayout make_dec_layout(const mea_desc& d) {
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes); return o; };
   L.a = take(row * 2 * 4);
   L.q = take(row);
-  L.k = take(row);
-  L.v = take(row);
   L.sig = take(row);
   L.o = take(row);
   L.part = take((size_t)(d.B * d.H) * L.S * (size_t)(d.N + 4) * 4);
@@ -700,8 +698,6 @@ int decode_launch(const mea_desc* d, const void* x, const void* wq, const void* 
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* a = at<float>(ws, L.a);
   bf16_bits* q = at<bf16_bits>(ws, L.q);
-  bf16_bits* k = at<bf16_bits>(ws, L.k);
-  bf16_bits* v = at<bf16_bits>(ws, L.v);
   bf16_bits* sig = at<bf16_bits>(ws, L.sig);
   bf16_bits* o = at<bf16_bits>(ws, L.o);
   // Projections of the B new tokens (a few rows: every weight row is read
@@ -728,9 +724,10 @@ int decode_launch(const mea_desc* d, const void* x, const void* wq, const void* 
   pp.f2 = f2;
   pp.pos = pos;
   pp.q = q;
-  pp.k = k;
-  pp.v = v;
+  pp.k_cache = static_cast<bf16_bits*>(k_cache);
+  pp.v_cache = static_cast<bf16_bits*>(v_cache);
   pp.sig = sig;
+  pp.Tc = (int)d->T;
   pp.B = B;
   pp.C = C;
   pp.H = (int)d->H;
@@ -741,8 +738,6 @@ int decode_launch(const mea_desc* d, const void* x, const void* wq, const void* 
   MEA_TRY(timed(K_DECODE_PROJ, s, [&] { return mea::launch_decode_proj_epilogue(pp, N, s); }));
   mea::DecodeParams dp;
   dp.q = q;
-  dp.k_new = k;
-  dp.v_new = v;
   dp.k_cache = static_cast<bf16_bits*>(k_cache);
   dp.v_cache = static_cast<bf16_bits*>(v_cache);
   dp.pos = pos;
@@ -753,7 +748,6 @@ int decode_launch(const mea_desc* d, const void* x, const void* wq, const void* 
   dp.Tc = (int)d->T;
   dp.S = L.S;
   dp.chunk = L.chunk;
-  MEA_TRY(timed(K_KV_APPEND, s, [&] { return mea::launch_kv_append(dp, N, s); }));
   MEA_TRY(timed(K_ATTN_DECODE, s, [&] { return mea::launch_attn_decode(dp, N, s); }));
   MEA_TRY(timed(K_DECODE_COMBINE, s, [&] { return mea::launch_attn_decode_combine(dp, N, s); }));
   // y = (O * sigmoid(g)) W_o^T for the B tokens.

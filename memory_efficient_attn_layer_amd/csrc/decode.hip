@@ -3,8 +3,8 @@
 // The reference is a training kernel and has no decode path; this is the
 // same block math (README.md:42-64) for the last row of a causal sequence
 // whose earlier k / v rows are cached: the new token's q, k, v come from the
-// projection kernel (at rotary row pos[b]), its k / v are appended to the
-// cache, and
+// projection epilogue (at rotary row pos[b]), which writes its k / v straight
+// into cache row pos[b], and
 //   O[b, h] = sum_{t <= pos[b]} 2^(q'.k_t - m) v_t / sum_{t <= pos[b]} 2^(q'.k_t - m)
 // with q' = q * log2(e) / sqrt(N) as the projection stores it.
 //
@@ -29,18 +29,6 @@ constexpr int kTargetWaves = 4096;  // splits over all (b, h) to fill the GPU
 
 __device__ __forceinline__ int clamp_pos(const DecodeParams& p, int b) {
   return min(max(p.pos[b], 0), p.Tc - 1);
-}
-
-// k_new / v_new row (b, h) -> cache row pos[b]; one thread per 16-byte chunk.
-__global__ __launch_bounds__(256) void kv_append_kernel(DecodeParams p, int N) {
-  const int CH = N / 8;
-  const int id = blockIdx.x * 256 + threadIdx.x;
-  if (id >= p.B * p.H * CH) return;
-  const int bh = id / CH, ch = id - bh * CH, b = bh / p.H;
-  const size_t dst = ((size_t)bh * p.Tc + clamp_pos(p, b)) * N + ch * 8;
-  const size_t src = (size_t)bh * N + ch * 8;
-  st16(p.k_cache + dst, ld16(p.k_new + src));
-  st16(p.v_cache + dst, ld16(p.v_new + src));
 }
 
 template <int N>
@@ -134,7 +122,9 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void attn_decode_kernel(DecodePa
 // gi takes splits gi, gi + G, ...; thread n of a group accumulates element
 // n (coalesced reads of each partial), and the groups' sums meet in LDS.
 // Split 0 always holds key 0, so M is finite; empty splits carry m = -inf
-// and weigh 0.
+// and weigh 0. (A last-workgroup-combines form inside the attention kernel
+// needs a device-scope release per workgroup, an L2 write-back on this
+// GPU; it made the attention 4x slower.)
 template <int N>
 __global__ __launch_bounds__(256) void attn_decode_combine_kernel(DecodeParams p) {
   constexpr int G = 256 / N;
@@ -272,7 +262,8 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // The same steps as the projection epilogue of the full-sequence kernel:
 // a = rx * (x W^T) with rx = rsqrt(mean(x^2) + eps) (fast_triton_attn.py:
 // 29-32), per-head RMSNorm of q and k (:102-106), rotary (:132-141) at row
-// pos[b], q times qscale, v plain, sigmoid(g) (:123).
+// pos[b], q times qscale, v plain, sigmoid(g) (:123). k and v go straight to
+// cache row pos[b] (clamped to [0, Tc - 1]), where the attention reads them.
 template <int N>
 __global__ __launch_bounds__(N) void decode_proj_epilogue_kernel(DecodeProjParams p) {
   __shared__ float red[N / 64 > 1 ? N / 64 : 1];
@@ -292,10 +283,10 @@ __global__ __launch_bounds__(N) void decode_proj_epilogue_kernel(DecodeProjParam
   const int row = min(max(p.pos[b], 0), p.t_max - 1);
   const float f1 = p.f1[(size_t)row * N + n], f2 = p.f2[(size_t)row * N + n];
   const float qsw = shfl_xor(qh, 1), ksw = shfl_xor(kh, 1);
-  const size_t o = (size_t)bh * N + n;
-  p.q[o] = f2bf((qh * f1 + qsw * f2) * p.qscale);
-  p.k[o] = f2bf(kh * f1 + ksw * f2);
-  p.v[o] = f2bf(av);
+  p.q[(size_t)bh * N + n] = f2bf((qh * f1 + qsw * f2) * p.qscale);
+  const size_t c = ((size_t)bh * p.Tc + min(max(p.pos[b], 0), p.Tc - 1)) * N + n;
+  p.k_cache[c] = f2bf(kh * f1 + ksw * f2);
+  p.v_cache[c] = f2bf(av);
   p.sig[(size_t)b * HN + h * N + n] = f2bf(1.0f / (1.0f + __expf(-ag)));
 }
 
@@ -334,12 +325,6 @@ void decode_splits(int B, int H, int Tc, int* S, int* chunk) {
   ch = (ch + 63) / 64 * 64;
   *S = s;
   *chunk = ch;
-}
-
-hipError_t launch_kv_append(const DecodeParams& p, int N, hipStream_t s) {
-  const int n = p.B * p.H * (N / 8);
-  hipLaunchKernelGGL(kv_append_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p, N);
-  return hipGetLastError();
 }
 
 hipError_t launch_attn_decode(const DecodeParams& p, int N, hipStream_t s) {

@@ -184,8 +184,7 @@ hipError_t launch_zero_f32(float* p, size_t n, hipStream_t s);
 // attends to cache rows 0 .. pos[b] (its own k / v included).
 struct DecodeParams {
   const bf16_bits* q;                       // (B, H, N) stored q (log2 units)
-  const bf16_bits *k_new, *v_new;           // (B, H, N) the new token's k, v
-  bf16_bits *k_cache, *v_cache;             // (B, H, Tc, N)
+  bf16_bits *k_cache, *v_cache;             // (B, H, Tc, N), the new token's rows already written
   const int* pos;                           // (B); clamped to [0, Tc - 1]
   float* part;                              // (B*H, S, N + 4): o[N], m, l per split
   bf16_bits* o;                             // (B, H*N) attention output
@@ -218,14 +217,14 @@ struct DecodeProjParams {
   const bf16_bits* x;                       // (B, C)
   const float *f1, *f2;                     // (t_max, N)
   const int* pos;                           // (B)
-  bf16_bits *q, *k, *v;                     // (B, H, N)
+  bf16_bits* q;                             // (B, H, N)
+  bf16_bits *k_cache, *v_cache;             // (B, H, Tc, N): k, v go to row pos[b] (clamped to [0, Tc - 1])
   bf16_bits* sig;                           // (B, HN)
-  int B, C, H, t_max;
+  int B, C, H, t_max, Tc;
   float eps, qscale;
   float inv_n;  // 1 / head dimensions in use (head RMSNorm mean)
 };
 hipError_t launch_decode_proj_epilogue(const DecodeProjParams& p, int N, hipStream_t s);
-hipError_t launch_kv_append(const DecodeParams& p, int N, hipStream_t s);
 hipError_t launch_attn_decode(const DecodeParams& p, int N, hipStream_t s);
 hipError_t launch_attn_decode_combine(const DecodeParams& p, int N, hipStream_t s);
 

@@ -155,7 +155,7 @@ def _decode_launch(x3, weights, factor1, factor2, H, N, n_active, pos, cache, ep
 
 class DecodeGraph:
     """``decode_step`` captured once in a HIP graph for a fixed batch, cache and
-    set of weights, then replayed: one graph launch per step instead of seven
+    set of weights, then replayed: one graph launch per step instead of five
     kernel launches and the Python around them. ``step(x, pos)`` copies x
     (B, C) and pos (B,) into the graph's static inputs, replays, and returns
     the static output (overwritten by the next step; clone it to keep it).
