@@ -107,6 +107,8 @@ BLOCK_CASES = [
     ("c1280-h5-b2-t100", _w("c1280", 2, 100, 1280, 5, 64), None),
     ("c2048-h16-n128-yarn8-b1-t256", _w("c2048", 1, 256, 2048, 16, 128, 8.0, 64), None),
     ("c3072-h4-b1-t64", _w("c3072", 1, 64, 3072, 4, 64), None),
+    # The widest model the library accepts (four dx feature groups; C > H*N).
+    ("c4096-h4-n128-b1-t48", _w("c4096", 1, 48, 4096, 4, 128), None),
     # C a multiple of 64 but not of 256 (any head count H at C = H*N): dx runs
     # the next wider layout with the features past C masked, the output
     # projection and dW end in partial 256-feature tiles.
