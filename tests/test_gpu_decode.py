@@ -87,6 +87,24 @@ def test_decode_at_position_zero_is_the_token_alone():
         assert_out_close(f"b{b}", y[b], _oracle_last(x[b:b + 1], ws, f1, f2, H, N))
 
 
+def test_decode_batch_past_one_token_tile():
+    # B = 70 new tokens: the decode products take a second 64-token tile, and
+    # 140 (b, h) pairs each get their own position (rewinds included).
+    C, H, N, B, T0, cap = 128, 2, 64, 70, 24, 32
+    ws, f1, f2, g = _params(C, H, N, cap, seed=17)
+    blk = _Block(ws, f1, f2, H, N)
+    x = torch.randn(B, T0, C, generator=g).bfloat16()
+    cache = KVCache.empty(B, H, N, cap, "cuda")
+    blk.prefill(x, cache)
+    pos = torch.randint(0, T0 + 1, (B,), generator=g).tolist()
+    xn = torch.randn(B, C, generator=g).bfloat16()
+    y = blk.decode(xn, pos, cache)
+    for b in range(B):
+        p = pos[b]
+        ref = _oracle_last(torch.cat([x[b, :p], xn[b:b + 1]]), ws, f1, f2, H, N)
+        assert_out_close(f"b{b} pos {p}", y[b], ref)
+
+
 def test_decode_long_cache_across_split_boundaries():
     # 3000 cache rows over B * H = 4 heads: 48 splits of 64 keys, so these
     # positions put the last key first, last and inside a split, and the
