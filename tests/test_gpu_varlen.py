@@ -53,6 +53,8 @@ def _oracle(inp, lens, H, N):
     ys, dxs, acc = [], [], {}
     t0 = 0
     for L in lens:
+        if L == 0:
+            continue  # an empty sequence contributes nothing
         part = {k: v for k, v in inp.items()}
         part["x"] = inp["x"][t0:t0 + L][None]
         part["dy"] = inp["dy"][t0:t0 + L][None]
@@ -70,8 +72,8 @@ def _oracle(inp, lens, H, N):
 @pytest.mark.parametrize(
     "lens,C,H,N",
     [([77, 256, 300, 1, 513], 256, 2, 64), ([130, 64, 200], 512, 4, 128), ([90, 33, 160], 512, 2, 256),
-     ([70, 130], 96, 3, 32)],
-    ids=["n64-5seq", "n128-3seq", "n256-3seq", "n32-2seq"],
+     ([70, 130], 96, 3, 32), ([0, 90, 0, 0, 45], 256, 2, 64)],
+    ids=["n64-5seq", "n128-3seq", "n256-3seq", "n32-2seq", "n64-empty-seqs"],
 )
 def test_varlen_forward_backward_matches_oracle_per_sequence(lens, C, H, N):
     inp = _inputs(lens, C, H, N, t_max=max(lens) + 40, seed=21)
