@@ -63,6 +63,17 @@ typedef struct mea_desc {
                        in Wo and in the rotary tables are zero); the head
                        RMSNorm then averages over N_active dimensions and the
                        attention scale is 1/sqrt(N_active). */
+  int64_t tables_bf16; /* nonzero: every value in rows 0..T-1 of f1 and f2 is a
+                          bf16 number (the caller's tables were bf16, the only
+                          table dtype the reference runs with,
+                          fast_triton_attn.py:110-111). mea_fwd, mea_bwd, their
+                          varlen forms and mea_prefill then pack those rows
+                          into a bf16 copy in the workspace (T * N * 4 more
+                          bytes) that the projection epilogue reads, one
+                          16-byte load per 4 features of both tables; results
+                          are bitwise the same as with 0. Other values would be
+                          rounded to bf16 by the copy. The stage entry points
+                          and mea_decode read the fp32 tables either way. */
 } mea_desc;
 
 enum {

@@ -34,6 +34,7 @@ class MeaDesc(ctypes.Structure):
         ("T_max", ctypes.c_int64),
         ("eps", ctypes.c_float),
         ("N_active", ctypes.c_int64),
+        ("tables_bf16", ctypes.c_int64),
     ]
 
 
@@ -122,9 +123,12 @@ def check(code: int, what: str) -> None:
         raise RuntimeError(f"{what} failed: {strerror(code)} (status {code})")
 
 
-def desc(B: int, T: int, C: int, H: int, N: int, T_max: int, eps: float, N_active: int = 0) -> MeaDesc:
-    """A descriptor; N_active > 0: heads of N_active dimensions carried zero-padded to N."""
-    return MeaDesc(int(B), int(T), int(C), int(H), int(N), int(T_max), float(eps), int(N_active))
+def desc(B: int, T: int, C: int, H: int, N: int, T_max: int, eps: float, N_active: int = 0,
+         tables_bf16: bool = False) -> MeaDesc:
+    """A descriptor; N_active > 0: heads of N_active dimensions carried zero-padded to N;
+    tables_bf16: the fp32 tables passed hold bf16 values (the caller's tables were bf16)."""
+    return MeaDesc(int(B), int(T), int(C), int(H), int(N), int(T_max), float(eps), int(N_active),
+                   int(bool(tables_bf16)))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -105,6 +105,12 @@ def _tables32(factor1: torch.Tensor, factor2: torch.Tensor, T: int):
     return factor1[:T].float().contiguous(), factor2[:T].float().contiguous()
 
 
+def _bf16_tables(factor1: torch.Tensor, factor2: torch.Tensor) -> bool:
+    """Whether the fp32 copies of the tables hold bf16 numbers only (the
+    library then reads a packed bf16 copy in the projection; same results)."""
+    return factor1.dtype == torch.bfloat16 and factor2.dtype == torch.bfloat16
+
+
 def _wants_grad(*tensors) -> bool:
     """Whether autograd will record the op: grad mode is on and an input
     requires grad. Decided by the caller of ``Function.apply``: inside
@@ -145,7 +151,7 @@ class FusedAttentionFunction(torch.autograd.Function):
         xc = x.contiguous()
         wc = [w.contiguous() for w in weights]
         f1, f2 = _tables32(factor1, factor2, T)
-        d = _lib.desc(B, T, C, H, N, T, eps, n_active)
+        d = _lib.desc(B, T, C, H, N, T, eps, n_active, _bf16_tables(factor1, factor2))
         y = torch.empty((B, T, C), device=dev, dtype=torch.bfloat16)
         if need_bwd:
             o_save = torch.empty((B, T, H * N), device=dev, dtype=torch.bfloat16)
@@ -174,7 +180,7 @@ class FusedAttentionFunction(torch.autograd.Function):
         dev = x.device
         dy = grad_output.to(torch.bfloat16).contiguous()
         f1, f2 = _tables32(factor1, factor2, T)
-        d = _lib.desc(B, T, C, H, N, T, eps, ctx.n_active)
+        d = _lib.desc(B, T, C, H, N, T, eps, ctx.n_active, _bf16_tables(factor1, factor2))
         dx = torch.empty_like(x)
         dws = [torch.empty_like(w) for w in (wq, wk, wv, wg, wo)]
         want_f = ctx.needs_input_grad[6] or ctx.needs_input_grad[7]
@@ -268,8 +274,9 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         wc = [w.contiguous() for w in weights]
         cu = cu_seqlens.contiguous()
         f1, f2 = _tables32(factor1, factor2, max_len)
-        d = _lib.desc(1, total, C, H, N, max_len, eps, n_active)
-        d_ws = _lib.desc(1, total, C, H, N, total, eps, n_active)
+        tb16 = _bf16_tables(factor1, factor2)
+        d = _lib.desc(1, total, C, H, N, max_len, eps, n_active, tb16)
+        d_ws = _lib.desc(1, total, C, H, N, total, eps, n_active, tb16)
         y = torch.empty((total, C), device=dev, dtype=torch.bfloat16)
         if need_bwd:
             o_save = torch.empty((total, H * N), device=dev, dtype=torch.bfloat16)
@@ -302,8 +309,9 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         nseq = cu.numel() - 1
         dy = grad_output.to(torch.bfloat16).contiguous()
         f1, f2 = _tables32(factor1, factor2, max_len)
-        d = _lib.desc(1, total, C, H, N, max_len, eps, ctx.n_active)
-        d_ws = _lib.desc(1, total, C, H, N, total, eps, ctx.n_active)
+        tb16 = _bf16_tables(factor1, factor2)
+        d = _lib.desc(1, total, C, H, N, max_len, eps, ctx.n_active, tb16)
+        d_ws = _lib.desc(1, total, C, H, N, total, eps, ctx.n_active, tb16)
         dx = torch.empty_like(x)
         dws = [torch.empty_like(w) for w in (wq, wk, wv, wg, wo)]
         want_f = ctx.needs_input_grad[6] or ctx.needs_input_grad[7]

@@ -20,6 +20,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // Byte offsets of every transient inside the workspace.
 struct Layout {
   size_t q, k, v, sig, tpos, o, qkn;         // forward (tpos: packed sequences only)
+  size_t rot;                                // packed bf16 tables (tables_bf16 only)
   size_t dO, daq, dag;                       // backward (da_k, da_v overwrite k, v)
   size_t rx, rq, rk, delta, woT, wcatT, part;
   size_t tpart;                              // table-gradient partials (MEA_PASS_BWD_TABLES)
@@ -37,6 +38,9 @@ Layout make_layout(const mea_desc& d, int pass) {
   L.v = take(act);
   L.sig = take(act);
   L.tpos = take(M * 4);
+  // Rows 0 .. T-1 (packed sequences: max_len <= T) of both tables, 8 bytes
+  // per (row, feature).
+  if (d.tables_bf16 != 0) L.rot = take((size_t)d.T * (size_t)d.N * 4);
   if (pass == MEA_PASS_FWD) {
     L.o = take(act);
     L.qkn = take(2 * sizeof(float));
@@ -136,12 +140,12 @@ T* at(void* ws, size_t off) {
 enum KernelId {
   K_QKVG_PROJ, K_ATTN_FWD, K_GATE_OPROJ, K_TRANSPOSE, K_ZERO, K_DZ_GATE_BWD,
   K_ATTN_BWD_DQ, K_ATTN_BWD_DKDV, K_DW_PARTIAL, K_DW_REDUCE, K_DX,
-  K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_REDUCE, K_COUNT
+  K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_REDUCE, K_ROTARY_PACK, K_COUNT
 };
 const char* const kKernelNames[K_COUNT] = {
     "qkvg_proj", "attn_fwd", "gate_oproj", "transpose", "zero_f32", "dz_gate_bwd",
     "attn_bwd_dq", "attn_bwd_dkdv", "dw_partial", "dw_reduce", "dx",
-    "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad_reduce"};
+    "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad_reduce", "rotary_pack"};
 
 struct ProfRec {
   int kernel;
@@ -202,9 +206,11 @@ float q_log2_scale(int64_t N) { return (float)(1.4426950408889634 / sqrt((double
 int64_t n_active(const mea_desc* d) { return d->N_active != 0 ? d->N_active : d->N; }
 
 // Launch sequence pieces; the public entry points validate before calling.
+// Packed tables (tabp, tab_rows rows; see pack_tables) or null: f1 / f2.
 int proj_launch(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
                 const float* f1, const float* f2, void* q, void* k, void* v, void* sig, float* rx, float* rq,
-                float* rk, float qscale, float* qk_norm2, const int* tpos, void* stream) {
+                float* rk, float qscale, float* qk_norm2, const int* tpos, const bf16_bits* tabp, int tab_rows,
+                void* stream) {
   mea::ProjParams p;
   p.x = static_cast<const bf16_bits*>(x);
   p.wq = static_cast<const bf16_bits*>(wq);
@@ -213,6 +219,7 @@ int proj_launch(const mea_desc* d, const void* x, const void* wq, const void* wk
   p.wg = static_cast<const bf16_bits*>(wg);
   p.f1 = f1;
   p.f2 = f2;
+  p.tabp = tabp;
   p.q = static_cast<bf16_bits*>(q);
   p.k = static_cast<bf16_bits*>(k);
   p.v = static_cast<bf16_bits*>(v);
@@ -223,7 +230,7 @@ int proj_launch(const mea_desc* d, const void* x, const void* wq, const void* wk
   p.qk_norm2 = qk_norm2;
   p.qscale = qscale;
   p.tpos = tpos;
-  p.t_max = (int)d->T_max;
+  p.t_max = tabp != nullptr ? tab_rows : (int)d->T_max;
   p.M = (int)(d->B * d->T);
   p.T = (int)d->T;
   p.C = (int)d->C;
@@ -242,7 +249,8 @@ int proj_impl(const mea_desc* d, const void* x, const void* wq, const void* wk, 
   if (rc != MEA_OK) return rc;
   rc = check_ptrs({x, wq, wk, wv, wg, f1, f2, q, k, v, sig});
   if (rc != MEA_OK) return rc;
-  return proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, qscale, qk_norm2, nullptr, stream);
+  return proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, qscale, qk_norm2, nullptr, nullptr, 0,
+                     stream);
 }
 
 }  // namespace
@@ -324,6 +332,22 @@ int mea_gate_oproj(const mea_desc* d, const void* o, const void* sig, const void
 
 namespace {
 
+// With d->tables_bf16: packs the table rows the projection reads (0 .. T-1;
+// packed sequences 0 .. max_len-1) into the workspace and returns the copy in
+// *tabp and its row count in *rows; otherwise *tabp = null.
+hipError_t pack_tables(const mea_desc* d, const Varlen* var, const float* f1, const float* f2, void* ws,
+                       const Layout& L, hipStream_t s, const bf16_bits** tabp, int* rows) {
+  *tabp = nullptr;
+  *rows = 0;
+  if (d->tables_bf16 == 0) return hipSuccess;
+  bf16_bits* out = at<bf16_bits>(ws, L.rot);
+  const int n = var != nullptr ? var->max_len : (int)d->T;
+  const hipError_t e = timed(K_ROTARY_PACK, s, [&] { return mea::launch_rotary_pack(f1, f2, n, (int)d->N, out, s); });
+  *tabp = out;
+  *rows = n;
+  return e;
+}
+
 int fwd_impl(const mea_desc* d, const Varlen* var, const void* x, const void* wq, const void* wk, const void* wv,
              const void* wg, const void* wo, const float* f1, const float* f2, void* y, void* o_save,
              float* lse_save, void* ws, size_t ws_bytes, void* stream) {
@@ -351,7 +375,11 @@ int fwd_impl(const mea_desc* d, const Varlen* var, const void* x, const void* wq
     tpos = at<int>(ws, L.tpos);
     MEA_TRY(mea::launch_token_positions(var->cu, var->nseq, (int)d->T, tpos, static_cast<hipStream_t>(stream)));
   }
-  rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, nullptr, nullptr, nullptr, qs, qkn, tpos, stream);
+  const bf16_bits* tabp;
+  int tab_rows;
+  MEA_TRY(pack_tables(d, var, f1, f2, ws, L, static_cast<hipStream_t>(stream), &tabp, &tab_rows));
+  rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, nullptr, nullptr, nullptr, qs, qkn, tpos, tabp,
+                   tab_rows, stream);
   if (rc != MEA_OK) return rc;
   rc = attn_fwd_launch(d, q, k, v, o, lse_save, 1.0f, qkn, var, stream);
   if (rc != MEA_OK) return rc;
@@ -413,8 +441,11 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
     tpos = at<int>(ws, L.tpos);
     MEA_TRY(mea::launch_token_positions(var->cu, var->nseq, T, tpos, s));
   }
+  const bf16_bits* tabp;
+  int tab_rows;
+  MEA_TRY(pack_tables(d, var, f1, f2, ws, L, s, &tabp, &tab_rows));
   int rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, bf.q, bf.k, bf.v, bf.sig, bf.rx, bf.rq, bf.rk, qs, nullptr, tpos,
-                       stream);
+                       tabp, tab_rows, stream);
   if (rc != MEA_OK) return rc;
 
   mea::DzParams dz;

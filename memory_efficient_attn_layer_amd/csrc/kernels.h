@@ -14,6 +14,10 @@ struct ProjParams {
   const bf16_bits* x;                       // (M, C)
   const bf16_bits *wq, *wk, *wv, *wg;       // (H*N, C)
   const float *f1, *f2;                     // (T_max, N)
+  // Packed bf16 copy of the tables (t_max rows of N / 4 16-byte words, word
+  // n / 4 of row t = f1[t, n..n+3], f2[t, n..n+3]), or null: the epilogue
+  // then reads f1 / f2. Used when every table value is a bf16 number.
+  const bf16_bits* tabp;
   bf16_bits *q, *k, *v;                     // (B, H, T, N)
   bf16_bits* sig;                           // (M, H*N)
   float* rx;                                // (M) or null
@@ -24,13 +28,17 @@ struct ProjParams {
   // Rotary row of every token (M), or null (row = t of the (B, T) layout):
   // packed sequences give each token its position inside its sequence.
   const int* tpos;
-  int t_max;                                // rows of f1 / f2 (tpos is clamped to it)
+  int t_max;                                // rows of f1 / f2 or tabp (tpos is clamped to it)
   int M, T, C, H;
   float eps;
   float qscale;                             // the stored q rows are q * qscale
   float inv_n;                              // 1 / head dimensions in use (head RMSNorm mean)
 };
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s);
+
+// tabp (ProjParams) from rows 0 .. rows-1 of f1 and f2: values rounded to
+// bf16, so exact for tables whose values are bf16 numbers.
+hipError_t launch_rotary_pack(const float* f1, const float* f2, int rows, int N, bf16_bits* tabp, hipStream_t s);
 
 // tpos[m] = m - cu[s] for cu[s] <= m < cu[s+1] (packed sequences).
 hipError_t launch_token_positions(const int* cu, int nseq, int M, int* tpos, hipStream_t s);

@@ -57,7 +57,9 @@ __device__ __forceinline__ ProjTile proj_tile(int L, int H) {
 // XCD work on neighbouring tiles at the same time.
 // POS: every token reads its rotary row from p.tpos (packed sequences); a
 // separate instantiation, so the (B, T) kernel keeps its code.
-template <int N, bool POS>
+// PK: the epilogue reads the packed bf16 tables p.tabp (one 16-byte load per
+// 4 features for both tables) instead of the fp32 f1 / f2 rows (two).
+template <int N, bool POS, bool PK>
 __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   constexpr int BT = kProjBT, BF = kProjBF, BK = kProjBK, NS = kProjStages;
   constexpr int STAGE = (BF + BT) * BK;
@@ -76,7 +78,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   constexpr int LOADS = (BF + BT) * BK / 8 / 64 / 4;  // load instructions per wave per slab
   __shared__ __attribute__((aligned(16))) bf16_bits smem[NS * STAGE];
   __shared__ float ssq_s[BT];
-  __shared__ float xch[HALF ? 2 : 1][HALF ? 2 : 1][HALF ? BT : 1];  // [ss | norm][wf][token] (HALF)
+  __shared__ float xch[2][HALF ? 2 : 1][HALF ? BT : 1];  // [ss | norm][wf][token] (HALF)
 
   // Locals, not captures of the argument block: a lambda holding &p would
   // force the block into scratch memory.
@@ -228,14 +230,34 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     // as block tb consumes it. N = 128 (twice the rows) reads each feature
     // block's rows just before use.
     constexpr bool PREF = N == 64;
-    f32x4 tab1[PREF ? GF : 1], tab2[PREF ? GF : 1];
+    constexpr bool SLOT32 = PREF && !PK, SLOTW = PREF && PK;
+    f32x4 tab1[SLOT32 ? GF : 1], tab2[SLOT32 ? GF : 1];
+    u32x4 tabw[SLOTW ? GF : 1];
+    // Features col + 16j + 4g .. +3 of block tb's token: fp32 row of f, or
+    // the packed word (row t, features n..n+3) = 16-byte word t * N/4 + n/4.
     auto tab_at = [&](const float* f, int tb, int j) {
       return *reinterpret_cast<const f32x4*>(f + (size_t)tab_row(tb) * N + col + 16 * j + 4 * g);
     };
+    auto tabw_at = [&](int tb, int j) {
+      return *reinterpret_cast<const u32x4*>(p.tabp + 2 * ((size_t)tab_row(tb) * N + col + 16 * j + 4 * g));
+    };
     auto load_tab_j = [&](int tb, int j) {
-      if (PREF) {
-        tab1[PREF ? j : 0] = tab_at(p.f1, tb, j);
-        tab2[PREF ? j : 0] = tab_at(p.f2, tb, j);
+      if (SLOTW) {
+        tabw[SLOTW ? j : 0] = tabw_at(tb, j);
+      } else if (SLOT32) {
+        tab1[SLOT32 ? j : 0] = tab_at(p.f1, tb, j);
+        tab2[SLOT32 ? j : 0] = tab_at(p.f2, tb, j);
+      }
+    };
+    // (f1, f2) of those features, from the slot (N = 64) or from memory.
+    auto tab_vals = [&](int tb, int j, f32x4& a1, f32x4& a2) {
+      if (PK) {
+        const u32x4 w = SLOTW ? tabw[SLOTW ? j : 0] : tabw_at(tb, j);
+        a1 = f32x4{lo_bf(w[0]), hi_bf(w[0]), lo_bf(w[1]), hi_bf(w[1])};
+        a2 = f32x4{lo_bf(w[2]), hi_bf(w[2]), lo_bf(w[3]), hi_bf(w[3])};
+      } else {
+        a1 = SLOT32 ? tab1[SLOT32 ? j : 0] : tab_at(p.f1, tb, j);
+        a2 = SLOT32 ? tab2[SLOT32 ? j : 0] : tab_at(p.f2, tb, j);
       }
     };
 
@@ -357,8 +379,10 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
 #pragma unroll
       for (int j = 0; j < GF; ++j) {
         const int n = 16 * j + 4 * g;
-        const f32x4 a1 = (PREF ? tab1[PREF ? j : 0] : tab_at(p.f1, tb, j)) * sc;
-        const f32x4 a2 = (PREF ? tab2[PREF ? j : 0] : tab_at(p.f2, tb, j)) * sc;
+        f32x4 a1, a2;
+        tab_vals(tb, j, a1, a2);
+        a1 *= sc;
+        a2 *= sc;
         if (next >= 0) load_tab_j(next, j);
         const f32x4& a = acc[gi * GF + j][tb];
         float o[4];
@@ -472,21 +496,48 @@ int persistent_grid(int tiles, int per_cu) {
   return tiles < per_cu * cus[dev] ? tiles : per_cu * cus[dev];
 }
 
+template <int N>
+static void launch_proj_n(const ProjParams& p, int G, hipStream_t s) {
+  const bool pos = p.tpos != nullptr, pk = p.tabp != nullptr;
+  if (!pos && !pk)
+    hipLaunchKernelGGL((qkvg_proj_kernel<N, false, false>), dim3(G), dim3(256), 0, s, p);
+  else if (!pos)
+    hipLaunchKernelGGL((qkvg_proj_kernel<N, false, true>), dim3(G), dim3(256), 0, s, p);
+  else if (!pk)
+    hipLaunchKernelGGL((qkvg_proj_kernel<N, true, false>), dim3(G), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((qkvg_proj_kernel<N, true, true>), dim3(G), dim3(256), 0, s, p);
+}
+
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s) {
   const int G = persistent_grid(((p.M + kProjBT - 1) / kProjBT) * p.H * (4 * N / kProjBF), 2);
-  const bool pos = p.tpos != nullptr;
-  if (N == 64 && !pos)
-    hipLaunchKernelGGL((qkvg_proj_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
-  else if (N == 64)
-    hipLaunchKernelGGL((qkvg_proj_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
-  else if (N == 128 && !pos)
-    hipLaunchKernelGGL((qkvg_proj_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
+  if (N == 64)
+    launch_proj_n<64>(p, G, s);
   else if (N == 128)
-    hipLaunchKernelGGL((qkvg_proj_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
-  else if (!pos)
-    hipLaunchKernelGGL((qkvg_proj_kernel<256, false>), dim3(G), dim3(256), 0, s, p);
+    launch_proj_n<128>(p, G, s);
   else
-    hipLaunchKernelGGL((qkvg_proj_kernel<256, true>), dim3(G), dim3(256), 0, s, p);
+    launch_proj_n<256>(p, G, s);
+  return hipGetLastError();
+}
+
+namespace {
+
+// One thread per 4-feature group i = t * N/4 + n/4 of rows 0 .. rows-1:
+// (f1[4i .. 4i+3], f2[4i .. 4i+3]) rounded to bf16 into word i.
+__global__ __launch_bounds__(256) void rotary_pack_kernel(const f32x4* f1, const f32x4* f2, int groups, u32x4* out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= groups) return;
+  const f32x4 a = f1[i], b = f2[i];
+  out[i] = u32x4{pack2(a[0], a[1]), pack2(a[2], a[3]), pack2(b[0], b[1]), pack2(b[2], b[3])};
+}
+
+}  // namespace
+
+hipError_t launch_rotary_pack(const float* f1, const float* f2, int rows, int N, bf16_bits* tabp, hipStream_t s) {
+  const int groups = rows * (N / 4);
+  hipLaunchKernelGGL(rotary_pack_kernel, dim3((groups + 255) / 256), dim3(256), 0, s,
+                     reinterpret_cast<const f32x4*>(f1), reinterpret_cast<const f32x4*>(f2), groups,
+                     reinterpret_cast<u32x4*>(tabp));
   return hipGetLastError();
 }
 

@@ -92,8 +92,9 @@ def prefill(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor
     dev = x.device
     xc = x.contiguous()
     wc = [w.contiguous() for w in weights]
+    tb16 = factor1.dtype == torch.bfloat16 and factor2.dtype == torch.bfloat16
     f1, f2 = _tables(factor1, factor2, Tc)
-    d = _lib.desc(B, T, C, H, N, Tc, eps, n_active)
+    d = _lib.desc(B, T, C, H, N, Tc, eps, n_active, tb16)
     y = torch.empty((B, T, C), device=dev, dtype=torch.bfloat16)
     ws_bytes = lib.mea_workspace_bytes(d, _lib.MEA_PASS_FWD)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)

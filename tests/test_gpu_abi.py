@@ -81,3 +81,93 @@ def test_guarded_forward_backward(w):
         assert_grad_close(k, t.view(shp), ref[k])
     assert_grad_close("df1", df1.view(T, N), ref["df1"])
     assert_grad_close("df2", df2.view(T, N), ref["df2"])
+
+
+PACK_CASES = [Workload(99, "n64", 2, 200, 256, 2, 64), Workload(99, "n128", 1, 130, 512, 4, 128),
+              Workload(99, "n256", 1, 96, 512, 2, 256)]
+WS_GUARD = 4096  # bytes on each side of the workspace (a multiple of 256 keeps it aligned)
+
+
+def _ws_guarded(nbytes):
+    buf = torch.full((nbytes + 2 * WS_GUARD,), 0xA5, dtype=torch.uint8, device="cuda")
+    return buf, buf[WS_GUARD:WS_GUARD + nbytes]
+
+
+def _ws_intact(buf):
+    return bool((buf[:WS_GUARD] == 0xA5).all() and (buf[-WS_GUARD:] == 0xA5).all())
+
+
+def _bits(t):
+    return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
+
+
+def _run_block(lib, g, f1, f2, w, tables_bf16, var=None):
+    """mea_fwd + mea_bwd (or their varlen forms with var = (cu, nseq, max_len))
+    with table gradients; workspaces guarded. Returns every output."""
+    B, T, C, H, N = w.B, w.T, w.C, w.H, w.N
+    HN, M = H * N, B * T
+    t_max = var[2] if var is not None else T
+    d = _lib.desc(B, T, C, H, N, t_max, 1e-6, 0, tables_bf16)
+    d_ws = _lib.desc(B, T, C, H, N, T, 1e-6, 0, tables_bf16)
+    s = _lib.stream_of(torch.device("cuda"))
+    wts = [g[n].data_ptr() for n in ("wq", "wk", "wv", "wg", "wo")]
+    y = torch.empty(M * C, dtype=torch.bfloat16, device="cuda")
+    o = torch.empty(M * HN, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(B * H * T, dtype=torch.float32, device="cuda")
+    nf = lib.mea_workspace_bytes(ctypes.byref(d_ws), _lib.MEA_PASS_FWD)
+    wsf_buf, wsf = _ws_guarded(nf)
+    head = (var[0].data_ptr(), var[1], var[2]) if var is not None else ()
+    fwd = lib.mea_fwd_varlen if var is not None else lib.mea_fwd
+    rc = fwd(ctypes.byref(d), *head, g["x"].data_ptr(), *wts, f1.data_ptr(), f2.data_ptr(), y.data_ptr(),
+             o.data_ptr(), lse.data_ptr(), wsf.data_ptr(), nf, s)
+    assert rc == 0, _lib.strerror(rc)
+    rows = t_max
+    dx = torch.empty(M * C, dtype=torch.bfloat16, device="cuda")
+    dws = [torch.empty(HN * C, dtype=torch.bfloat16, device="cuda") for _ in range(5)]
+    df1 = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    df2 = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    nb = lib.mea_workspace_bytes(ctypes.byref(d_ws), _lib.MEA_PASS_BWD_TABLES)
+    wsb_buf, wsb = _ws_guarded(nb)
+    bwd = lib.mea_bwd_varlen if var is not None else lib.mea_bwd
+    rc = bwd(ctypes.byref(d), *head, g["dy"].data_ptr(), g["x"].data_ptr(), *wts, f1.data_ptr(), f2.data_ptr(),
+             o.data_ptr(), lse.data_ptr(), dx.data_ptr(), *(t.data_ptr() for t in dws), df1.data_ptr(),
+             df2.data_ptr(), wsb.data_ptr(), nb, s)
+    assert rc == 0, _lib.strerror(rc)
+    torch.cuda.synchronize()
+    assert _ws_intact(wsf_buf) and _ws_intact(wsb_buf), "write past the workspace"
+    return dict(y=y, o=o, lse=lse, dx=dx, dwq=dws[0], dwk=dws[1], dwv=dws[2], dwg=dws[3], dwo=dws[4],
+                df1=df1, df2=df2)
+
+
+@pytest.mark.parametrize("w", PACK_CASES, ids=[f"B{w.B}-T{w.T}-C{w.C}-H{w.H}-N{w.N}" for w in PACK_CASES])
+def test_packed_bf16_tables_bitwise(w):
+    """tables_bf16 = 1 (the projection reads a packed bf16 copy of tables whose
+    values are bf16 numbers) gives bitwise the outputs of tables_bf16 = 0 in
+    the forward and the backward, inside the workspace it asks for."""
+    lib = _lib.load()
+    inp = make_inputs(w)  # bf16 tables
+    g = {k: v.cuda().contiguous() for k, v in inp.items()}
+    f1, f2 = g["f1"].float().contiguous(), g["f2"].float().contiguous()
+    plain = _run_block(lib, g, f1, f2, w, False)
+    packed = _run_block(lib, g, f1, f2, w, True)
+    for k in plain:
+        assert torch.equal(_bits(plain[k]), _bits(packed[k])), f"{k} differs with packed tables"
+    assert torch.isfinite(plain["y"].float()).all()
+
+
+def test_packed_bf16_tables_varlen_bitwise():
+    """The packed-sequence forms with tables_bf16 = 1 (per-token rotary rows
+    read from the packed copy of max_len rows) match tables_bf16 = 0 bitwise."""
+    lib = _lib.load()
+    lens = [70, 0, 131, 33]
+    w = Workload(99, "varlen", 1, sum(lens), 256, 2, 64)
+    inp = make_inputs(w)
+    g = {k: v.cuda().contiguous() for k, v in inp.items()}
+    max_len = max(lens)
+    f1, f2 = g["f1"][:max_len].float().contiguous(), g["f2"][:max_len].float().contiguous()
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
+    var = (cu, len(lens), max_len)
+    plain = _run_block(lib, g, f1, f2, w, False, var)
+    packed = _run_block(lib, g, f1, f2, w, True, var)
+    for k in plain:
+        assert torch.equal(_bits(plain[k]), _bits(packed[k])), f"{k} differs with packed tables"

@@ -66,6 +66,12 @@ def test_workspace_bytes(lib):
     # Table gradients need per-token partials: B * T * 2N fp32 more.
     tab = lib.mea_workspace_bytes(ctypes.byref(_d()), _lib.MEA_PASS_BWD_TABLES)
     assert tab - bwd >= M * 2 * 64 * 4
+    # bf16-valued tables: a packed bf16 copy of T rows (8 bytes per row and
+    # feature) in every pass's workspace.
+    for ps in (_lib.MEA_PASS_FWD, _lib.MEA_PASS_BWD, _lib.MEA_PASS_BWD_TABLES):
+        d16 = _lib.desc(2, 256, 256, 4, 64, 256, 1e-6, 0, True)
+        plain = lib.mea_workspace_bytes(ctypes.byref(_d()), ps)
+        assert lib.mea_workspace_bytes(ctypes.byref(d16), ps) - plain == 256 * 64 * 4
     # Invalid descriptors report 0.
     for bad in (_d(N=96), _d(C=300), _d(T_max=10), _d(eps=0.0), _d(B=0)):
         assert lib.mea_workspace_bytes(ctypes.byref(bad), 0) == 0
