@@ -142,6 +142,26 @@ def test_decode_matches_prefill_rows():
         assert_out_close(f"t{t}", y, y_pre[:, t])
 
 
+@pytest.mark.parametrize("C,H,N", [(256, 2, 64), (512, 4, 128)], ids=["n64", "n128"])
+def test_prefill_with_bf16_tables_is_bitwise_the_fp32_copy(C, H, N):
+    # bf16 tables take the packed-table projection; their fp32 copy the plain
+    # one. Same values, so the outputs and both caches agree bitwise.
+    B, T0, cap = 2, 75, 96
+    ws, f1, f2, g = _params(C, H, N, cap, seed=23)
+    f1b, f2b = f1.bfloat16(), f2.bfloat16()
+    x = torch.randn(B, T0, C, generator=g).bfloat16()
+    outs = []
+    for t1, t2 in ((f1b, f2b), (f1b.float(), f2b.float())):
+        cache = KVCache.empty(B, H, N, cap, "cuda")
+        y = prefill(x.cuda(), *[w.cuda() for w in ws], t1.cuda(), t2.cuda(), H, N, cache)
+        torch.cuda.synchronize()
+        outs.append((y, cache.k.clone(), cache.v.clone()))
+    for name, a, b in zip(("y", "k_cache", "v_cache"), outs[0], outs[1]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), name
+    ref = ob.block_forward(x.float(), *(w.float() for w in ws), f1b.float(), f2b.float(), H, N)
+    assert_out_close("y", outs[0][0], ref)
+
+
 @pytest.mark.parametrize("C,H,N", [(512, 4, 128), (128, 4, 32)], ids=["n128", "n32-padded"])
 def test_decode_graph_replays_match_eager_steps(C, H, N):
     # Captured decode steps, replayed several times with eager work and
