@@ -579,6 +579,10 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
   dxp.x = static_cast<const bf16_bits*>(x);
   dxp.rx = bf.rx;
   dxp.dx = static_cast<bf16_bits*>(dx);
+  // 768 < C <= 1024: feature groups of 512 over 128 tokens, group 0's
+  // uncorrected rows parked in the recomputed q buffer (dead after the
+  // attention backward; M x HN >= M x 512 elements).
+  dxp.scratch = C > 768 && C <= 1024 && HN >= 512 ? bf.q : nullptr;
   dxp.M = M;
   dxp.C = C;
   dxp.HN = HN;

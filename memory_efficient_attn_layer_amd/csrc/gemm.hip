@@ -227,9 +227,21 @@ __device__ __forceinline__ const bf16_bits* da_part(const DaParts& dp, int part)
 // C = p.C is a multiple of 32 with CP - 256 < C <= CP. Weight rows past C - 1
 // read row C - 1, x columns past the row are clamped into it, accumulators of
 // features past C are zeroed before the dot, and their stores are skipped.
+//
+// GROUPS = 2 (CP = 512, 768 < C <= 1024): the 512-feature layout over 128
+// tokens walks the features in two groups, so each weight slab is re-read
+// per 128 tokens rather than per 64 (the 1024-wide layout holds 64 tokens).
+// The dot (acc . x) is summed over both groups in LDS. Group 0 leaves its
+// uncorrected acc as bf16 in p.scratch (M x 512; the reference's dx_hat is a
+// bf16 matmul output too, fast_triton_attn.py:655-660), group 1 writes its
+// result, then every thread re-reads the scratch chunks it stored, applies
+// the correction and writes those dx chunks (a thread's own store is visible
+// to its own later load once vmcnt has drained). da_g may live in dx: each
+// workgroup writes only its own rows, after both groups have read them.
 // ---------------------------------------------------------------------------
-template <int CP>
+template <int CP, int GROUPS = 1>
 __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP / 128) : 1)), 1) void dx_kernel(DxParams p) {
+  static_assert(GROUPS == 1 || CP == 512, "feature groups use the 512-wide layout");
   constexpr int WF = CP / 128;                          // waves along features
   constexpr int WT = 8 % WF == 0 ? 8 / WF : 1;          // waves along tokens
   constexpr int NW = WF * WT;
@@ -244,6 +256,7 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
   constexpr int SMEM = NS * STAGE > NW * XW ? NS * STAGE : NW * XW;
   __shared__ __attribute__((aligned(16))) bf16_bits smem[SMEM];
   __shared__ float dotp[WF][BT];
+  __shared__ float dsum[GROUPS > 1 ? BT : 1];  // dot summed over the groups
 
   const int M = p.M, C = p.C, K4 = 4 * p.HN;
   const int m0 = xcd_remap(blockIdx.x, (M + BT - 1) / BT) * BT;
@@ -266,11 +279,17 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
   int hmf[Plan::NU];
 #pragma unroll
   for (int u = 0; u < Plan::NU; ++u) hmf[u] = __builtin_amdgcn_readfirstlane(hm(mf(u)));
+  if (GROUPS > 1 && tid < BT) dsum[GROUPS > 1 ? tid : 0] = 0.f;
+  const uint32_t lds0 = lds_addr(smem);
+  const float inv_c = 1.0f / (float)C;
 
+#pragma unroll 1
+  for (int grp = 0; grp < GROUPS; ++grp) {
+  const int f0 = grp * CP;  // first feature of the group
+  const bool last = grp == GROUPS - 1;
   // Slabs are issued in order ks = 0, 1, 2, ...; (part, hh, n0) locate the
   // next one: part of da, head, first column within the head.
   int part = 0, hh = 0, n0 = 0;
-  const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int ks, int st) {
     const uint32_t lds = lds0 + (uint32_t)(st * STAGE) * 2u;
     // The weight slab is one contiguous C x 32 block: 1 KB per load
@@ -278,8 +297,8 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
     // row offset non-negative).
     const bf16_bits* wslab = wt_g + (size_t)ks * C * BK;
     slab_issue<CP, NW, BK>(
-        lds, wave, BK, [&](int u) { return wslab + (size_t)min(u * NW * 16, C - 1) * BK; },
-        [&](int u, int i) { return min(u * NW * 16 + i, C - 1) - min(u * NW * 16, C - 1); });
+        lds, wave, BK, [&](int u) { return wslab + (size_t)min(f0 + u * NW * 16, C - 1) * BK; },
+        [&](int u, int i) { return min(f0 + u * NW * 16 + i, C - 1) - min(f0 + u * NW * 16, C - 1); });
     {
       const bool tokm = part == 3;
       const bf16_bits* src = da_part(dp, part);
@@ -339,15 +358,21 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
   // c ^ (r & 15), so the accumulator-layout reads below (lane: one token,
   // 4 features) are conflict-free. Each wave reads only its own block.
   __syncthreads();  // every wave is past its last slab read
+  // With GROUPS > 1 the lane index is opaque to the compiler inside each
+  // group, so the epilogue's lane-constant offsets are recomputed per group
+  // rather than hoisted out of the group loop and held across it.
+  int lane_e = lane;
+  if (GROUPS > 1) asm volatile("" : "+v"(lane_e));
+  const int c16e = lane_e & 15, ge = lane_e >> 4;
   bf16_bits* xs = smem + wave * XW;
   int mrow[TB];
   float rxr[TB];
-  if (wf * 128 + 128 > C) {
+  if (f0 + wf * 128 + 128 > C) {
     // Features 16 fb + 4 g .. + 3 past C: their accumulators (products with
     // the clamped weight row) must not enter the dot (wave-uniform branch).
 #pragma unroll
     for (int fb = 0; fb < FB; ++fb) {
-      const bool out = wf * 128 + 16 * fb + 4 * g >= C;
+      const bool out = f0 + wf * 128 + 16 * fb + 4 * ge >= C;
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) acc[fb][tb] = out ? zero4() : acc[fb][tb];
     }
@@ -358,20 +383,20 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
     const uint32_t lds = lds_addr(xs);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int r = 4 * j + (lane >> 4), ch = (lane & 15) ^ (r & 15);
-      const int col = min(wf * 128 + ch * 8, C - 8);  // columns past the row: clamped, never used
+      const int r = 4 * j + (lane_e >> 4), ch = (lane_e & 15) ^ (r & 15);
+      const int col = min(f0 + wf * 128 + ch * 8, C - 8);  // columns past the row: clamped, never used
       const uint32_t voff = (uint32_t)((min(m0 + wt * 64 + r, M - 1) - r0) * C + col) * 2u;
       g2lds16_s(xb, voff, lds + (uint32_t)j * 1024u);
     }
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
-      mrow[tb] = min(m0 + wt * 64 + tb * 16 + c16, M - 1);
+      mrow[tb] = min(m0 + wt * 64 + tb * 16 + c16e, M - 1);
       rxr[tb] = p.rx[mrow[tb]];
     }
   }
   // Features 16 fb + 4 g .. + 3 of token row r of the wave's block.
   auto xs_at = [&](int r, int fb) {
-    return reinterpret_cast<u32x2*>(xs + r * 128 + (((2 * fb + (g >> 1)) ^ (r & 15)) << 3) + 4 * (g & 1));
+    return reinterpret_cast<u32x2*>(xs + r * 128 + (((2 * fb + (ge >> 1)) ^ (r & 15)) << 3) + 4 * (ge & 1));
   };
   wait_vmcnt0();  // this wave's x block has landed
 
@@ -382,29 +407,41 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
     float d = 0.f;
 #pragma unroll
     for (int fb = 0; fb < FB; ++fb) {
-      const u32x2 xw = *xs_at(tb * 16 + c16, fb);
+      const u32x2 xw = *xs_at(tb * 16 + c16e, fb);
       d += acc[fb][tb][0] * lo_bf(xw[0]) + acc[fb][tb][1] * hi_bf(xw[0]) + acc[fb][tb][2] * lo_bf(xw[1]) +
            acc[fb][tb][3] * hi_bf(xw[1]);
     }
     d += shfl_xor(d, 16);
     d += shfl_xor(d, 32);
-    if (g == 0) dotp[wf][wt * 64 + tb * 16 + c16] = d;
+    if (ge == 0) dotp[wf][wt * 64 + tb * 16 + c16e] = d;
   }
   __syncthreads();
+  if (GROUPS > 1) {
+    if (tid < BT) {
+      float t = dsum[GROUPS > 1 ? tid : 0];
+#pragma unroll
+      for (int i = 0; i < WF; ++i) t += dotp[i][tid];
+      dsum[GROUPS > 1 ? tid : 0] = t;
+    }
+    __syncthreads();
+  }
 
   // dx = acc - x rx^2 (acc . x) / C, written over the x values it consumes
   // (each lane overwrites exactly the 8 bytes it read), then stored per 16
-  // tokens as whole 256-byte row segments.
-  const float inv_c = 1.0f / (float)C;
+  // tokens as whole 256-byte row segments. An earlier group stores acc.
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) {
     float dot = 0.f;
+    if (GROUPS > 1) {
+      dot = dsum[GROUPS > 1 ? wt * 64 + tb * 16 + c16e : 0];
+    } else {
 #pragma unroll
-    for (int i = 0; i < WF; ++i) dot += dotp[i][wt * 64 + tb * 16 + c16];
-    const float cf = rxr[tb] * rxr[tb] * dot * inv_c;
+      for (int i = 0; i < WF; ++i) dot += dotp[i][wt * 64 + tb * 16 + c16e];
+    }
+    const float cf = last ? rxr[tb] * rxr[tb] * dot * inv_c : 0.f;
 #pragma unroll
     for (int fb = 0; fb < FB; ++fb) {
-      u32x2* xp = xs_at(tb * 16 + c16, fb);
+      u32x2* xp = xs_at(tb * 16 + c16e, fb);
       const u32x2 xw = *xp;
       const f32x4& a = acc[fb][tb];
       const float o0 = a[0] - lo_bf(xw[0]) * cf, o1 = a[1] - hi_bf(xw[0]) * cf;
@@ -414,10 +451,41 @@ __global__ __launch_bounds__(64 * ((CP / 128) * (8 % (CP / 128) == 0 ? 8 / (CP /
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's writes are done
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int r = tb * 16 + it * 4 + (lane >> 4), ch = lane & 15;
+      const int r = tb * 16 + it * 4 + (lane_e >> 4), ch = lane_e & 15;
       const int m = m0 + wt * 64 + r;
       const u32x4 val = *reinterpret_cast<const u32x4*>(xs + r * 128 + ((ch ^ (r & 15)) << 3));
-      if (m < M && wf * 128 + ch * 8 < C) st16(p.dx + (size_t)m * C + wf * 128 + ch * 8, val);
+      if (!last) {
+        if (m < M) st16(p.scratch + (size_t)m * CP + wf * 128 + ch * 8, val);
+      } else if (m < M && f0 + wf * 128 + ch * 8 < C)
+        st16(p.dx + (size_t)m * C + f0 + wf * 128 + ch * 8, val);
+    }
+  }
+  if (GROUPS > 1) __syncthreads();  // the x blocks are the next group's slab ring
+  }  // groups
+
+  if constexpr (GROUPS > 1) {
+    // Group 0's features (all below 512 < C): reload the acc chunks this
+    // thread stored, correct them, write dx.
+    wait_vmcnt0();
+    int lane_c = lane;
+    asm volatile("" : "+v"(lane_c));
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int r = tb * 16 + it * 4 + (lane_c >> 4), ch = lane_c & 15;
+        const int m = m0 + wt * 64 + r;
+        if (m >= M) continue;
+        const int col = wf * 128 + ch * 8;
+        const float rxv = p.rx[m];
+        const float cf = rxv * rxv * dsum[wt * 64 + r] * inv_c;
+        float a[8], xv[8], o[8];
+        unpack8(ld16(p.scratch + (size_t)m * CP + col), a);
+        unpack8(ld16(p.x + (size_t)m * C + col), xv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = a[e] - xv[e] * cf;
+        st16(p.dx + (size_t)m * C + col, pack8(o));
+      }
     }
   }
 }
@@ -628,6 +696,8 @@ hipError_t launch_dx(const DxParams& p, hipStream_t s) {
     hipLaunchKernelGGL(dx_kernel<512>, dim3((p.M + 127) / 128), dim3(512), 0, s, p);
   else if (p.C <= 768)
     hipLaunchKernelGGL(dx_kernel<768>, dim3((p.M + 63) / 64), dim3(384), 0, s, p);
+  else if (p.C <= 1024 && p.scratch != nullptr)
+    hipLaunchKernelGGL((dx_kernel<512, 2>), dim3((p.M + 127) / 128), dim3(512), 0, s, p);
   else if (p.C <= 1024)
     hipLaunchKernelGGL(dx_kernel<1024>, dim3((p.M + 63) / 64), dim3(512), 0, s, p);
   else

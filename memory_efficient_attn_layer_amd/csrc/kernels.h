@@ -142,6 +142,9 @@ struct DxParams {
   const bf16_bits* x;                       // (M, C)
   const float* rx;                          // (M)
   bf16_bits* dx;                            // (M, C)
+  // (M, 512) bf16 for 768 < C <= 1024 (feature groups of 512), or null: the
+  // 1024-wide layout over 64 tokens runs instead.
+  bf16_bits* scratch;
   int M, C, HN;
 };
 hipError_t launch_dx(const DxParams& p, hipStream_t s);

@@ -118,6 +118,11 @@ BLOCK_CASES = [
     ("c64-h1-b2-t100", _w("c64", 2, 100, 64, 1, 64), None),
     ("c320-ne-hn-h2-n128-b1-t64", _w("c320", 1, 64, 320, 2, 128), None),
     ("c1344-h21-b1-t80", _w("c1344", 1, 80, 1344, 21, 64), None),
+    # 768 < C <= 1024 with H*N >= 512: dx walks two 512-feature groups over
+    # 128 tokens (the second partial here), da_g in dx (H*N <= C) or in its
+    # own buffer (H*N > C); 300 tokens end in a partial block.
+    ("c800-hn512-b2-t150", _w("c800", 2, 150, 800, 8, 64), None),
+    ("c928-hn1024-n128-b1-t300", _w("c928", 1, 300, 928, 8, 128), None),
     # Heads of 32 and 16 dimensions (carried zero-padded to 64; the head
     # RMSNorm and the attention scale use the true width).
     ("n32-h8-c256-b2-t100", _w("n32", 2, 100, 256, 8, 32), None),
