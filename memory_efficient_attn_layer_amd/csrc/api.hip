@@ -21,6 +21,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 struct Layout {
   size_t q, k, v, sig, tpos, o, qkn;         // forward (tpos: packed sequences only)
   size_t rot;                                // packed bf16 tables (tables_bf16 only)
+  size_t wpk;                                // k-slab-major copies of Wq, Wk, Wv, Wg
   size_t dO, daq, dag;                       // backward (da_k, da_v overwrite k, v)
   size_t rx, rq, rk, delta, woT, wcatT, part;
   size_t tpart;                              // table-gradient partials (MEA_PASS_BWD_TABLES)
@@ -41,6 +42,7 @@ Layout make_layout(const mea_desc& d, int pass) {
   // Rows 0 .. T-1 (packed sequences: max_len <= T) of both tables, 8 bytes
   // per (row, feature).
   if (d.tables_bf16 != 0) L.rot = take((size_t)d.T * (size_t)d.N * 4);
+  L.wpk = take(4 * HN * C * 2);
   if (pass == MEA_PASS_FWD) {
     L.o = take(act);
     L.qkn = take(2 * sizeof(float));
@@ -140,12 +142,12 @@ T* at(void* ws, size_t off) {
 enum KernelId {
   K_QKVG_PROJ, K_ATTN_FWD, K_GATE_OPROJ, K_TRANSPOSE, K_ZERO, K_DZ_GATE_BWD,
   K_ATTN_BWD_DQ, K_ATTN_BWD_DKDV, K_DW_PARTIAL, K_DW_REDUCE, K_DX,
-  K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_REDUCE, K_ROTARY_PACK, K_COUNT
+  K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_REDUCE, K_ROTARY_PACK, K_WEIGHT_PACK, K_COUNT
 };
 const char* const kKernelNames[K_COUNT] = {
     "qkvg_proj", "attn_fwd", "gate_oproj", "transpose", "zero_f32", "dz_gate_bwd",
     "attn_bwd_dq", "attn_bwd_dkdv", "dw_partial", "dw_reduce", "dx",
-    "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad_reduce", "rotary_pack"};
+    "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad_reduce", "rotary_pack", "weight_pack"};
 
 struct ProfRec {
   int kernel;
@@ -207,16 +209,21 @@ int64_t n_active(const mea_desc* d) { return d->N_active != 0 ? d->N_active : d-
 
 // Launch sequence pieces; the public entry points validate before calling.
 // Packed tables (tabp, tab_rows rows; see pack_tables) or null: f1 / f2.
+// wpk: the k-slab-major weight copies (see pack_weights) or null: the
+// row-major weights wq .. wg.
 int proj_launch(const mea_desc* d, const void* x, const void* wq, const void* wk, const void* wv, const void* wg,
                 const float* f1, const float* f2, void* q, void* k, void* v, void* sig, float* rx, float* rq,
                 float* rk, float qscale, float* qk_norm2, const int* tpos, const bf16_bits* tabp, int tab_rows,
-                void* stream) {
+                const bf16_bits* wpk, void* stream) {
   mea::ProjParams p;
   p.x = static_cast<const bf16_bits*>(x);
-  p.wq = static_cast<const bf16_bits*>(wq);
-  p.wk = static_cast<const bf16_bits*>(wk);
-  p.wv = static_cast<const bf16_bits*>(wv);
-  p.wg = static_cast<const bf16_bits*>(wg);
+  const size_t wsz = (size_t)(d->H * d->N) * (size_t)d->C;
+  p.wq = wpk != nullptr ? wpk : static_cast<const bf16_bits*>(wq);
+  p.wk = wpk != nullptr ? wpk + wsz : static_cast<const bf16_bits*>(wk);
+  p.wv = wpk != nullptr ? wpk + 2 * wsz : static_cast<const bf16_bits*>(wv);
+  p.wg = wpk != nullptr ? wpk + 3 * wsz : static_cast<const bf16_bits*>(wg);
+  p.w_row = wpk != nullptr ? 32 : (int)d->C;
+  p.w_slab = wpk != nullptr ? 32 * d->H * d->N : 32;
   p.f1 = f1;
   p.f2 = f2;
   p.tabp = tabp;
@@ -250,7 +257,7 @@ int proj_impl(const mea_desc* d, const void* x, const void* wq, const void* wk, 
   rc = check_ptrs({x, wq, wk, wv, wg, f1, f2, q, k, v, sig});
   if (rc != MEA_OK) return rc;
   return proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, rx, rq, rk, qscale, qk_norm2, nullptr, nullptr, 0,
-                     stream);
+                     nullptr, stream);
 }
 
 }  // namespace
@@ -348,6 +355,18 @@ hipError_t pack_tables(const mea_desc* d, const Varlen* var, const float* f1, co
   return e;
 }
 
+// Wq, Wk, Wv, Wg into k-slab-major copies in the workspace (2 * 4HN * C
+// bytes) for the projection's weight-slab loads; returns the copy.
+hipError_t pack_weights(const mea_desc* d, const void* wq, const void* wk, const void* wv, const void* wg, void* ws,
+                        const Layout& L, hipStream_t s, const bf16_bits** wpk) {
+  bf16_bits* out = at<bf16_bits>(ws, L.wpk);
+  mea::WcatPackParams wp{static_cast<const bf16_bits*>(wq), static_cast<const bf16_bits*>(wk),
+                         static_cast<const bf16_bits*>(wv), static_cast<const bf16_bits*>(wg), out,
+                         (int)(d->H * d->N), (int)d->C};
+  *wpk = out;
+  return timed(K_WEIGHT_PACK, s, [&] { return mea::launch_wslab_pack(wp, s); });
+}
+
 int fwd_impl(const mea_desc* d, const Varlen* var, const void* x, const void* wq, const void* wk, const void* wv,
              const void* wg, const void* wo, const float* f1, const float* f2, void* y, void* o_save,
              float* lse_save, void* ws, size_t ws_bytes, void* stream) {
@@ -378,8 +397,10 @@ int fwd_impl(const mea_desc* d, const Varlen* var, const void* x, const void* wq
   const bf16_bits* tabp;
   int tab_rows;
   MEA_TRY(pack_tables(d, var, f1, f2, ws, L, static_cast<hipStream_t>(stream), &tabp, &tab_rows));
+  const bf16_bits* wpk;
+  MEA_TRY(pack_weights(d, wq, wk, wv, wg, ws, L, static_cast<hipStream_t>(stream), &wpk));
   rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, q, k, v, sig, nullptr, nullptr, nullptr, qs, qkn, tpos, tabp,
-                   tab_rows, stream);
+                   tab_rows, wpk, stream);
   if (rc != MEA_OK) return rc;
   rc = attn_fwd_launch(d, q, k, v, o, lse_save, 1.0f, qkn, var, stream);
   if (rc != MEA_OK) return rc;
@@ -444,8 +465,10 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
   const bf16_bits* tabp;
   int tab_rows;
   MEA_TRY(pack_tables(d, var, f1, f2, ws, L, s, &tabp, &tab_rows));
+  const bf16_bits* wpk;
+  MEA_TRY(pack_weights(d, wq, wk, wv, wg, ws, L, s, &wpk));
   int rc = proj_launch(d, x, wq, wk, wv, wg, f1, f2, bf.q, bf.k, bf.v, bf.sig, bf.rx, bf.rq, bf.rk, qs, nullptr, tpos,
-                       tabp, tab_rows, stream);
+                       tabp, tab_rows, wpk, stream);
   if (rc != MEA_OK) return rc;
 
   mea::DzParams dz;

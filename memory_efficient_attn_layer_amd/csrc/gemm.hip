@@ -1077,6 +1077,29 @@ hipError_t launch_wcat_pack(const WcatPackParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+namespace {
+
+// One thread per 16-byte chunk of the packed output: matrix blockIdx.z,
+// k-slab kk, row r, chunk c8 (8 elements) <- row r, columns 32 kk + 8 c8.
+__global__ __launch_bounds__(256) void wslab_pack_kernel(WcatPackParams p) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // chunk index within one matrix
+  const int nch = p.HN * (p.C / 8);
+  if (i >= nch) return;
+  const int c8 = i & 3, r = (i >> 2) % p.HN, kk = (i >> 2) / p.HN;
+  const bf16_bits* w = blockIdx.z == 0 ? p.wq : blockIdx.z == 1 ? p.wk : blockIdx.z == 2 ? p.wv : p.wg;
+  const u32x4 v = ld16(w + (size_t)r * p.C + kk * 32 + c8 * 8);
+  *reinterpret_cast<u32x4*>(p.out + (size_t)blockIdx.z * p.HN * p.C + (size_t)i * 8) = v;
+}
+
+}  // namespace
+
+hipError_t launch_wslab_pack(const WcatPackParams& p, hipStream_t s) {
+  if (p.C % 32 != 0) return hipErrorInvalidValue;
+  const int nch = p.HN * (p.C / 8);
+  hipLaunchKernelGGL(wslab_pack_kernel, dim3((nch + 255) / 256, 1, 4), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void zero_f32_kernel(float* p, size_t n) {
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0.f;
 }

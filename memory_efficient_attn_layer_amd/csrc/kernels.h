@@ -12,7 +12,12 @@ typedef uint16_t bf16_bits;
 // Input RMSNorm + q/k/v/g projection + q/k head RMSNorm + rotary + sigmoid.
 struct ProjParams {
   const bf16_bits* x;                       // (M, C)
-  const bf16_bits *wq, *wk, *wv, *wg;       // (H*N, C)
+  // (H*N, C) weights: element (row, k) at row * w_row + (k / 32) * w_slab +
+  // k % 32. Row-major: w_row = C, w_slab = 32; the k-slab-major copy of
+  // launch_wslab_pack: w_row = 32, w_slab = 32 * H*N.
+  const bf16_bits *wq, *wk, *wv, *wg;
+  int w_row;
+  int64_t w_slab;
   const float *f1, *f2;                     // (T_max, N)
   // Packed bf16 copy of the tables (t_max rows of N / 4 16-byte words, word
   // n / 4 of row t = f1[t, n..n+3], f2[t, n..n+3]), or null: the epilogue
@@ -187,6 +192,12 @@ struct WcatPackParams {
   int HN, C;
 };
 hipError_t launch_wcat_pack(const WcatPackParams& p, hipStream_t s);
+
+// Each of Wq, Wk, Wv, Wg (HN, C) into k-slab-major (C / 32, HN, 32) at
+// out + i * HN * C (i = 0 q, 1 k, 2 v, 3 g): a 32-wide k-slab of any run of
+// rows is one contiguous block, so the projection's weight-slab loads read
+// 1 KB of contiguous memory per instruction.
+hipError_t launch_wslab_pack(const WcatPackParams& p, hipStream_t s);
 
 // Fills n floats with zero (a kernel, so it is safe inside captured graphs).
 hipError_t launch_zero_f32(float* p, size_t n, hipStream_t s);

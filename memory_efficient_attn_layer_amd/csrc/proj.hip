@@ -15,7 +15,11 @@
 //
 // Tile: 256 features x 128 tokens. k-slabs of 32 stream through a 3-stage
 // LDS ring filled by direct global->LDS loads, two slabs ahead, continuously
-// across the tiles a workgroup walks (one barrier per slab). Four waves of
+// across the tiles a workgroup walks (one barrier per slab). The block entry
+// points pass k-slab-major copies of the weights (a slab of a tile's rows is
+// one contiguous block, 1 KB per load instruction; from the row-major
+// matrices each instruction gathers 16 rows of 64 bytes): 0.714 -> 0.680 ms
+// per launch at B64 T4096 C512 H8 N64. Four waves of
 // 128 features x 64 tokens (32 accumulators of 16x16): for N = 64 a wave owns
 // one rotary projection (q or k) and one plain one (v or g) of its tokens, so
 // the epilogue work is the same in every wave. Two workgroups share a CU, so
@@ -84,6 +88,8 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   // force the block into scratch memory.
   const bf16_bits* __restrict__ xg = p.x;
   const bf16_bits *wq = p.wq, *wk = p.wk, *wv = p.wv, *wg = p.wg;
+  const int w_row = p.w_row;
+  const int64_t w_slab = p.w_slab;
   const int M = p.M, C = p.C, H = p.H, T = p.T, HN = H * N;
   const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   // offsets with the x rows clamped to the last token) is set when the
   // cursor enters a tile, so issuing a slab only adds its k offset.
   SlabPlan<BF, 4, BK> wplan;
-  slab_plan(wplan, wave, C, [](int, int i) { return i; });
+  slab_plan(wplan, wave, p.w_row, [](int, int i) { return i; });
   SlabPlan<BT, 4, BK> xplan;
   constexpr int NUW = SlabPlan<BF, 4, BK>::NU, NUX = SlabPlan<BT, 4, BK>::NU;
   const bf16_bits* wbase[NUW];
@@ -139,7 +145,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
 #pragma unroll
     for (int u = 0; u < NUW; ++u) {
       const int seg = (64 * u) / N;  // compile-time after unrolling
-      wbase[u] = wseg[seg] + (size_t)(tl.h * N + 64 * u - seg * N) * C;
+      wbase[u] = wseg[seg] + (size_t)(tl.h * N + 64 * u - seg * N) * w_row;
     }
 #pragma unroll
     for (int u = 0; u < NUX; ++u) xbase[u] = xg + (size_t)min(tl.m0 + 64 * u, M - 1) * C;
@@ -150,7 +156,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     const uint32_t lds = lds0 + (uint32_t)(iss_st * STAGE) * 2u;
     const int kk = iss_ks + iss_rot >= nk ? iss_ks + iss_rot - nk : iss_ks + iss_rot;
     const int k0 = kk * BK;
-    slab_issue_planned<BF, 4, BK>(lds, wave, wplan, [&](int u) { return wbase[u] + k0; });
+    slab_issue_planned<BF, 4, BK>(lds, wave, wplan, [&](int u) { return wbase[u] + kk * w_slab; });
     slab_issue_planned<BT, 4, BK>(lds + BF * BK * 2, wave, xplan, [&](int u) { return xbase[u] + k0; });
     iss_st = iss_st == NS - 1 ? 0 : iss_st + 1;
     if (++iss_ks == nk) {
