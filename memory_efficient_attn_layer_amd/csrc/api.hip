@@ -449,7 +449,7 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
   const Layout L = make_layout(*d, df1 != nullptr ? MEA_PASS_BWD_TABLES : MEA_PASS_BWD);
 
   // Weight transposes (k-contiguous B operands for dZ and dx).
-  MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_transpose(static_cast<const bf16_bits*>(wo), C, HN, HN, bf.woT, C, 0, s); }));
+  MEA_TRY(timed(K_TRANSPOSE, s, [&] { return mea::launch_transpose_slabs(static_cast<const bf16_bits*>(wo), C, HN, HN, bf.woT, s); }));
   {
     mea::WcatPackParams wp{static_cast<const bf16_bits*>(wq), static_cast<const bf16_bits*>(wk),
                            static_cast<const bf16_bits*>(wv), static_cast<const bf16_bits*>(wg), bf.wcatT, HN, C};

@@ -119,7 +119,7 @@ hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s);
 //                               projection's input, for dWo)
 struct DzParams {
   const bf16_bits* dy;                      // (M, C)
-  const bf16_bits* woT;                     // (HN, C)
+  const bf16_bits* woT;                     // Wo^T k-slab-major: (C / 32, HN, 32)
   const bf16_bits* o;                       // (M, HN)
   bf16_bits* sig;                           // (M, HN): sigmoid(a_g) in, z out
   const float* rx;                          // (M)
@@ -182,6 +182,9 @@ hipError_t launch_dw_reduce(const DwReduceParams& p, hipStream_t s);
 // column col_off.
 hipError_t launch_transpose(const bf16_bits* in, int rows, int cols, int ld_in, bf16_bits* out,
                             int ld_out, int col_off, hipStream_t s);
+// The same transpose stored k-slab-major: element (c, r) of out at
+// (r / 32) * cols * 32 + c * 32 + r % 32 (rows a multiple of 32).
+hipError_t launch_transpose_slabs(const bf16_bits* in, int rows, int cols, int ld_in, bf16_bits* out, hipStream_t s);
 
 // Wcat^T for dx in k-slab-major order: element (f, k) at
 // (k / 32) * C * 32 + f * 32 + k % 32, k over the stacked rows of

@@ -1,7 +1,10 @@
 // Token-block GEMM main loop for the memory-bound GEMMs of the block whose
 // output has at most 1024 features per token (output projection, dZ).
 //
-// D(f, t) = sum_k A(f, k) B(t, k): A is a row-major (NF, K) weight matrix,
+// D(f, t) = sum_k A(f, k) B(t, k): A is an (NF, K) weight matrix with
+// element (f, k) at f * a_row + (k / 32) * a_slab + k % 32 (row-major:
+// a_row = K, a_slab = 32; k-slab-major: a_row = 32, a_slab = 32 * rows;
+// (K / 32) * a_slab < 2^31),
 // B a row-major (M, K) activation matrix. Computed transposed like the other
 // token-major GEMMs: one workgroup covers all NF features of BT tokens, so
 // every activation row is read from HBM exactly once, and WF x WT waves own
@@ -46,7 +49,7 @@ __device__ __forceinline__ u32x4 gate8(const u32x4& a, const u32x4& b) {
 // (zeroed here). Rows of A past na - 1 read row na - 1 and rows of B past
 // M - 1 read row M - 1 (their results are not to be stored). K % 32 == 0.
 template <int NF, bool GATED>
-__device__ __forceinline__ void tok_mainloop(int K, bf16_bits* smem, const bf16_bits* A, int lda, int na,
+__device__ __forceinline__ void tok_mainloop(int K, bf16_bits* smem, const bf16_bits* A, int a_row, int a_slab, int na,
                                              const bf16_bits* B0, const bf16_bits* B1, int ldb, int m0, int M,
                                              f32x4 (&acc)[8][4]) {
   using S = TokShape<NF>;
@@ -63,7 +66,8 @@ __device__ __forceinline__ void tok_mainloop(int K, bf16_bits* smem, const bf16_
 #pragma unroll
     for (int i = 0; i < S::NA; ++i) {
       const int id = tid + S::NT * i;
-      if (S::A_CH % S::NT == 0 || id < S::A_CH) r.a[i] = ld16(A + (size_t)min(id >> 2, na - 1) * lda + k0 + (id & 3) * 8);
+      if (S::A_CH % S::NT == 0 || id < S::A_CH)
+        r.a[i] = ld16(A + (size_t)min(id >> 2, na - 1) * a_row + (uint32_t)((k0 / BK) * a_slab) + (id & 3) * 8);
     }
 #pragma unroll
     for (int i = 0; i < S::NB; ++i) {
