@@ -21,7 +21,7 @@ namespace mea {
 // ---------------------------------------------------------------------------
 // y = (O * sig) Wo^T, on the token-block main loop: A = Wo rows (output
 // features, k = HN), B = O * sig rows, gated while the slab is written to
-// LDS. Workgroup (x, y) covers the NF output features from y * NF of BT
+// LDS. A workgroup covers the NF output features from group * NF of BT
 // tokens (the last group may reach past C); y rows leave through an LDS
 // staging block as whole-row segments.
 // ---------------------------------------------------------------------------
@@ -32,7 +32,10 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void gate_oproj_kernel(OprojPa
   static_assert(S::NW * 16 * SP <= S::SMEM, "staging fits the slab stages");
   __shared__ __attribute__((aligned(16))) bf16_bits smem[S::SMEM];
   const int M = p.M, C = p.C, HN = p.HN;
-  const int m0 = xcd_remap(blockIdx.x, gridDim.x) * S::BT, f0 = blockIdx.y * NF;
+  // Workgroup (token block, feature group); the groups of one token block
+  // are consecutive on one XCD, so its O and sig rows come from HBM once.
+  const int ngrp = (C + NF - 1) / NF, lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int m0 = (lid / ngrp) * S::BT, f0 = (lid % ngrp) * NF;
   f32x4 acc[8][4];
   tok_mainloop<NF, true>(HN, smem, p.wo + (size_t)f0 * HN, HN, 32, min(NF, C - f0), p.o, p.sig, HN, m0, M, acc);
 
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void gate_oproj_kernel(OprojPa
 
 template <int NF>
 static void launch_oproj_nf(const OprojParams& p, hipStream_t s) {
-  const dim3 grid((p.M + TokShape<NF>::BT - 1) / TokShape<NF>::BT, (p.C + NF - 1) / NF);
+  const dim3 grid(((p.M + TokShape<NF>::BT - 1) / TokShape<NF>::BT) * ((p.C + NF - 1) / NF));
   hipLaunchKernelGGL(gate_oproj_kernel<NF>, grid, dim3(TokShape<NF>::NT), 0, s, p);
 }
 
@@ -80,8 +83,8 @@ hipError_t launch_gate_oproj(const OprojParams& p, hipStream_t s) {
 
 // ---------------------------------------------------------------------------
 // dZ = dy Wo with the gate backward in the epilogue, on the token-block main
-// loop: A = Wo^T rows (HN features, k = C), B = dy rows. Workgroup (x, y)
-// covers features y * NF .. y * NF + NF - 1 (clamped to HN; groups hold whole
+// loop: A = Wo^T rows (HN features, k = C), B = dy rows. A workgroup
+// covers features group * NF .. + NF - 1 (clamped to HN; groups hold whole
 // heads since NF is a multiple of N) of BT tokens. Each wave stages its fp32
 // dZ block per 16 tokens and walks it as rows: lane (row, 8-feature chunk)
 // loads sig and O, writes dO into the head-major (B, H, T, N) layout, da_g,
@@ -96,7 +99,10 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzPara
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM_BYTES];
   __shared__ float dpart[S::WF][S::BT];  // N = 256: each wave's half of delta
   const int M = p.M, C = p.C, H = p.H, T = p.T, N = p.N, HN = H * N;
-  const int m0 = xcd_remap(blockIdx.x, gridDim.x) * S::BT, f0 = blockIdx.y * NF;
+  // Workgroup (token block, feature group), the groups of a token block
+  // consecutive on one XCD (its dy rows come from HBM once).
+  const int ngrp = (HN + NF - 1) / NF, lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int m0 = (lid / ngrp) * S::BT, f0 = (lid % ngrp) * NF;
   f32x4 acc[8][4];
   // Wo^T is k-slab-major (C / 32, HN, 32): a slab of the group's rows is one
   // contiguous block (from row-major rows the loads ran 5.7% longer).
@@ -185,7 +191,7 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzPara
 
 template <int NF>
 static void launch_dz_nf(const DzParams& p, int HN, hipStream_t s) {
-  const dim3 grid((p.M + TokShape<NF>::BT - 1) / TokShape<NF>::BT, (HN + NF - 1) / NF);
+  const dim3 grid(((p.M + TokShape<NF>::BT - 1) / TokShape<NF>::BT) * ((HN + NF - 1) / NF));
   hipLaunchKernelGGL(dz_gate_bwd_kernel<NF>, grid, dim3(TokShape<NF>::NT), 0, s, p);
 }
 
