@@ -167,19 +167,19 @@ class FusedAttentionFunction(torch.autograd.Function):
             )
         _lib.check(rc, "mea_fwd")
         if need_bwd:
-            ctx.save_for_backward(xc, *wc, factor1, factor2, o_save, lse)
+            # The fp32 table rows too: the backward reuses them instead of casting again.
+            ctx.save_for_backward(xc, *wc, factor1, factor2, f1, f2, o_save, lse)
         ctx.H, ctx.N, ctx.eps, ctx.n_active = H, N, eps, n_active
         return y
 
     @staticmethod
     def backward(ctx, grad_output):
-        x, wq, wk, wv, wg, wo, factor1, factor2, o_save, lse = ctx.saved_tensors
+        x, wq, wk, wv, wg, wo, factor1, factor2, f1, f2, o_save, lse = ctx.saved_tensors
         H, N, eps = ctx.H, ctx.N, ctx.eps
         lib = _lib.load()
         B, T, C = x.shape
         dev = x.device
         dy = grad_output.to(torch.bfloat16).contiguous()
-        f1, f2 = _tables32(factor1, factor2, T)
         d = _lib.desc(B, T, C, H, N, T, eps, ctx.n_active, _bf16_tables(factor1, factor2))
         dx = torch.empty_like(x)
         dws = [torch.empty_like(w) for w in (wq, wk, wv, wg, wo)]
@@ -293,13 +293,13 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
             )
         _lib.check(rc, "mea_fwd_varlen")
         if need_bwd:
-            ctx.save_for_backward(xc, *wc, factor1, factor2, cu, o_save, lse)
+            ctx.save_for_backward(xc, *wc, factor1, factor2, f1, f2, cu, o_save, lse)
         ctx.H, ctx.N, ctx.eps, ctx.max_len, ctx.n_active = H, N, eps, max_len, n_active
         return y
 
     @staticmethod
     def backward(ctx, grad_output):
-        x, wq, wk, wv, wg, wo, factor1, factor2, cu, o_save, lse = ctx.saved_tensors
+        x, wq, wk, wv, wg, wo, factor1, factor2, f1, f2, cu, o_save, lse = ctx.saved_tensors
         H, N, eps, max_len = ctx.H, ctx.N, ctx.eps, ctx.max_len
         if x.shape[1] > MAX_C_BACKWARD:
             raise ValueError(f"backward supports C <= {MAX_C_BACKWARD}")
@@ -308,7 +308,6 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         dev = x.device
         nseq = cu.numel() - 1
         dy = grad_output.to(torch.bfloat16).contiguous()
-        f1, f2 = _tables32(factor1, factor2, max_len)
         tb16 = _bf16_tables(factor1, factor2)
         d = _lib.desc(1, total, C, H, N, max_len, eps, ctx.n_active, tb16)
         d_ws = _lib.desc(1, total, C, H, N, total, eps, ctx.n_active, tb16)
