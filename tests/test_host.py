@@ -333,3 +333,21 @@ def test_pad_heads_layout_and_gradients():
     assert torch.equal(ws[0].grad, gq.reshape(H, PAD_N, C)[:, :N].reshape(H * N, C))
     assert torch.equal(ws[4].grad, go.reshape(C, H, PAD_N)[:, :, :N].reshape(C, H * N))
     assert torch.equal(f1.grad, g1[:, :N])
+
+
+def test_bf16_table_flag_follows_table_dtype():
+    """The descriptor's tables_bf16 (packed bf16 table copy in the projection)
+    is set only when both tables are bf16, whose values the fp32 copies hold
+    exactly; fp16 and fp32 tables keep the fp32 reads."""
+    from memory_efficient_attn_layer_amd.attention import _bf16_tables
+
+    t = torch.zeros(8, 64)
+    assert _bf16_tables(t.bfloat16(), t.bfloat16())
+    for a, b in ((t, t), (t.half(), t.half()), (t.bfloat16(), t), (t.half(), t.bfloat16())):
+        assert not _bf16_tables(a, b)
+    d = _lib.desc(1, 8, 64, 1, 64, 8, 1e-6, 0, True)
+    assert d.tables_bf16 == 1 and _lib.desc(1, 8, 64, 1, 64, 8, 1e-6).tables_bf16 == 0
+    # Every bf16 number survives the round trip bf16 -> fp32 -> bf16 unchanged.
+    vals = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    finite = vals[torch.isfinite(vals)]
+    assert torch.equal(finite.float().bfloat16().view(torch.int16), finite.view(torch.int16))
