@@ -70,14 +70,24 @@ def kernel_work(w):
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (first processor entry of /proc/cpuinfo)."""
+    """The host CPU as /proc/cpuinfo names it: the full "model name" string of
+    the first processor entry, with its vendor, family, model and stepping
+    numbers (a virtual machine may report a shortened model name) and the
+    logical processors listed."""
     try:
+        fields, nproc = {}, 0
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key == "processor":
+                nproc += 1
+            if nproc == 1 and key in ("model name", "vendor_id", "cpu family", "model", "stepping"):
+                fields[key] = val.strip()
+        name = fields.get("model name", "unknown")
+        ids = ", ".join(f"{k} {fields[k]}" for k in ("vendor_id", "cpu family", "model", "stepping") if k in fields)
+        return f"{name} ({ids}; {nproc} logical processors in /proc/cpuinfo)"
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
 
 
 def cpu_baseline(w, seconds: float):
@@ -101,6 +111,7 @@ def cpu_baseline(w, seconds: float):
         if time.perf_counter() - t_start > 3 * seconds:
             break
     med = statistics.median(times)
+    per_seq = 3.4 * w.H * w.T * w.T * 4
     return {
         "value": w.T / med,
         "unit": "tokens/s",
@@ -108,7 +119,12 @@ def cpu_baseline(w, seconds: float):
         "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"fp32 oracle fwd+bwd (oracle/block.py) on 1 of {w.B} sequences (T={w.T}, C={w.C}, "
-                  f"H={w.H}, N={w.N}); 1 warm-up + {len(times)} timed iterations, median {med:.2f} s",
+                  f"H={w.H}, N={w.N}); 1 warm-up + {len(times)} timed iterations, median {med:.2f} s. "
+                  f"One sequence, because the oracle's math-path SDPA keeps fp32 (H, T, T) scores and "
+                  f"probabilities per sequence for the backward (about 3.4 H T^2 4 bytes = {per_seq / 1e9:.1f} GB "
+                  f"of host memory per sequence, measured 1.8 GB at T=4096, H=8; {w.B * per_seq / 1e9:.0f} GB "
+                  f"for all {w.B}); sequences are independent, so the cost is linear in B and value = T / median "
+                  f"is the per-token rate of the whole batch",
     }
 
 
@@ -207,7 +223,7 @@ def main():
     ap.add_argument("--no-eager", action="store_true",
                     help="skip the eager checkpoint+SDPA comparator (timed and peak HBM on the same GPU)")
     ap.add_argument("--table-grad", action="store_true",
-                    help="also differentiate the rotary tables (dF1 / dF2, as the reference always does)")
+                    help="also differentiate the (bf16) rotary tables (dF1 / dF2, as the reference always does)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-box-reference", action="store_true",
                     help="skip the vendor GEMM / copy speed reference (keeps kernel traces to this library)")
@@ -261,9 +277,11 @@ def main():
     f1, f2, dy = inp["f1"], inp["f2"], inp["dy"]
     wrt = [x, *ws]
     if args.table_grad:
-        # Trainable tables, differentiated like every other input.
-        f1 = f1.float().requires_grad_(True)
-        f2 = f2.float().requires_grad_(True)
+        # Trainable tables, differentiated like every other input. They stay
+        # bf16, as the reference's tables are, so the step differs from the
+        # plain one only by the table gradients (dF1 / dF2).
+        f1 = f1.detach().clone().requires_grad_(True)
+        f2 = f2.detach().clone().requires_grad_(True)
         wrt += [f1, f2]
     H, N = w.H, w.N
     sync = torch.cuda.synchronize

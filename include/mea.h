@@ -59,10 +59,14 @@ typedef struct mea_desc {
   int64_t N_active; /* head dimensions in use: 0 (all N), or 16 or 32 with N = 64.
                        No counterpart in the reference: a head of N_active < N
                        dimensions is carried zero-padded to N (the last
-                       N - N_active rows of every head in Wq, Wk, Wv, Wg, columns
-                       in Wo and in the rotary tables are zero); the head
-                       RMSNorm then averages over N_active dimensions and the
-                       attention scale is 1/sqrt(N_active). */
+                       N - N_active rows of every head in Wq, Wk, Wv, Wg and
+                       columns in Wo are zero; the last N - N_active columns of
+                       the rotary tables hold identity pairs, f1 = 1 and
+                       f2 = 0, as the Python wrapper pads them; zero columns
+                       are accepted too and give the same results, the
+                       backward mapping a zero 2x2 pair block to zero rows);
+                       the head RMSNorm then averages over N_active dimensions
+                       and the attention scale is 1/sqrt(N_active). */
   int64_t tables_bf16; /* nonzero: every value in rows 0..T-1 of f1 and f2 is a
                           bf16 number (the caller's tables were bf16, the only
                           table dtype the reference runs with,

@@ -338,20 +338,47 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         return (dx, *dws, gf1, gf2, None, None, None, None, None, None, None)
 
 
+def check_offsets(offsets, total: int) -> int:
+    """Host-side check of packed-sequence offsets: at least two entries,
+    starting at 0, nondecreasing, ending at ``total``. Returns the longest
+    sequence length."""
+    if len(offsets) < 2:
+        raise ValueError("cu_seqlens needs nseq + 1 >= 2 offsets")
+    if offsets[0] != 0 or offsets[-1] != total:
+        raise ValueError(f"cu_seqlens must run from 0 to {total} (got {offsets[0]} .. {offsets[-1]})")
+    lens = [b - a for a, b in zip(offsets[:-1], offsets[1:])]
+    if min(lens) < 0:
+        raise ValueError("cu_seqlens must be nondecreasing")
+    return max(lens)
+
+
 def fused_attn_varlen(x, q_proj, k_proj, v_proj, g_proj, o_proj, yarn_module, H, N, cu_seqlens, max_len=None,
                       eps=1e-6):
     """``fused_attn`` over packed sequences: x (total, C), cu_seqlens the
-    nseq + 1 int32 offsets (a device tensor, or a list of ints). max_len
-    defaults to the longest sequence (read from the offsets on the host)."""
+    nseq + 1 int32 offsets (a device tensor, a CPU tensor or a list of ints).
+    max_len defaults to the longest sequence (read from the offsets on the
+    host). Whenever the offsets are on the host (a list or a CPU tensor, or
+    read back because max_len was left out) they are checked: nondecreasing
+    from 0 to x.shape[0], and max_len at least the longest sequence (a
+    smaller one would leave that sequence's last rows unwritten). Offsets
+    passed on the device with an explicit max_len are trusted, as the C ABI
+    trusts them."""
     if not isinstance(cu_seqlens, torch.Tensor):
-        lens = list(cu_seqlens)
-        cu_seqlens = torch.tensor(lens, dtype=torch.int32, device=x.device)
-        host = lens
+        host = [int(v) for v in cu_seqlens]
+        cu_seqlens = torch.tensor(host, dtype=torch.int32, device=x.device)
+    elif cu_seqlens.device.type == "cpu":
+        host = [int(v) for v in cu_seqlens.tolist()]
+        cu_seqlens = cu_seqlens.to(device=x.device, dtype=torch.int32)
     else:
         host = None
-    if max_len is None:
-        host = host if host is not None else cu_seqlens.tolist()
-        max_len = max(b - a for a, b in zip(host[:-1], host[1:]))
+    if max_len is None and host is None:
+        host = [int(v) for v in cu_seqlens.tolist()]
+    if host is not None:
+        longest = check_offsets(host, x.shape[0])
+        if max_len is None:
+            max_len = longest
+        elif int(max_len) < longest:
+            raise ValueError(f"max_len={int(max_len)} is below the longest sequence ({longest} tokens)")
     return FusedAttentionVarlenFunction.apply(
         x, q_proj.weight, k_proj.weight, v_proj.weight, g_proj.weight, o_proj.weight, yarn_module.factor1,
         yarn_module.factor2, cu_seqlens, max_len, H, N, eps,

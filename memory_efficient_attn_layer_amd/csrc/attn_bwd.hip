@@ -108,7 +108,11 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
           const float det = a1[i] * a1[i + 1] - a2[i] * a2[i + 1];
-          const float inv = __builtin_amdgcn_rcpf(det);  // v_rcp_f32 (1 ulp): the IEEE division cost 0.8% of dQ
+          // v_rcp_f32 (1 ulp): the IEEE division cost 0.8% of dQ. A zero pair
+          // block (the padding columns of a narrow head given zero tables)
+          // maps its rows to zero, where the forward put them, not to
+          // 0 * inf = NaN.
+          const float inv = det != 0.f ? __builtin_amdgcn_rcpf(det) : 0.f;
           xh[i] = (a1[i + 1] * xv[i] - a2[i] * xv[i + 1]) * inv;
           xh[i + 1] = (a1[i] * xv[i + 1] - a2[i + 1] * xv[i]) * inv;
           dh[i] = a1[i] * dv[i] + a2[i + 1] * dv[i + 1];

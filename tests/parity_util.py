@@ -15,6 +15,8 @@ identical bf16-rounded inputs):
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from memory_efficient_attn_layer_amd.attention import FusedAttentionFunction
@@ -104,3 +106,50 @@ def check_block(w: Workload, B: int | None = None, seed: int | None = None, tabl
         assert_grad_close("df1", got["df1"][:T], ref["df1"][:T], scale=ref["dwv"])
         assert_grad_close("df2", got["df2"][:T], ref["df2"][:T], scale=ref["dwv"])
     return got, ref
+
+
+def early_daq_reference(inter: dict, dO: torch.Tensor, o_save: torch.Tensor, f1: torch.Tensor, f2: torch.Tensor,
+                        rx: torch.Tensor, H: int, N: int, E: int, eps: float = 1e-6) -> torch.Tensor:
+    """rx * dL/da_q for the query rows t < E, in float64, from the operands the
+    attention backward consumes: q as stored (bf16(c q) / c with
+    c = log2(e) / sqrt(N)), bf16 k and v (from the oracle's intermediates
+    ``inter``), the kernel's own dO (B, H, T, N) and its saved bf16 attention
+    output o_save (B, T, H*N) in delta = rowsum(dO * O). A flash backward's
+    delta comes from the bf16-rounded O, so sum_j dS_tj is not exactly zero and
+    a query that sees only a few keys keeps an error of relative size ~2^-9
+    times the cancellation of its dQ (up to 12% at t < 16); with every operand
+    taken as the kernel holds it, that error is in the reference too and the
+    rows agree to the normal row tolerance. Rows t < E depend on keys
+    0 .. E-1 only, so this costs E x E per head."""
+    B, T = rx.shape
+    E = min(E, T)
+    c = 1.4426950408889634 / math.sqrt(N)
+
+    def heads(t):  # (B, T, H, N) or (B, T, H*N) -> (B, H, E, N) float64
+        return t.detach().double().cpu().reshape(B, T, H, N)[:, :E].permute(0, 2, 1, 3)
+
+    def bf(t):
+        return t.bfloat16().double()
+
+    q = bf(heads(inter["q"]) * c) / c
+    k, v = bf(heads(inter["k"])), bf(heads(inter["v"]))
+    do = dO.detach().double().cpu()[:, :, :E]
+    o = heads(o_save)
+    s = (q @ k.transpose(-1, -2)) / math.sqrt(N)
+    s = s.masked_fill(~torch.ones(E, E, dtype=torch.bool).tril(), float("-inf"))
+    p = torch.softmax(s, -1)
+    ds = p * (do @ v.transpose(-1, -2) - (do * o).sum(-1, keepdim=True))
+    dq = (ds @ k) / math.sqrt(N)                                       # (B, H, E, N)
+    return q_chain(inter, dq, f1, f2, rx, eps)
+
+
+def q_chain(inter: dict, dq: torch.Tensor, f1: torch.Tensor, f2: torch.Tensor, rx: torch.Tensor,
+            eps: float = 1e-6) -> torch.Tensor:
+    """rx * dL/da_q (B, H, E, N) for dL/dq = dq (B, H, E, N) on the first E
+    rows: autograd through the oracle's head RMSNorm and rotary of a_q."""
+    B, T = rx.shape
+    E = dq.shape[2]
+    a_q = inter["a_q"].detach().double().cpu()[:, :E].clone().requires_grad_(True)  # (B, E, H, N)
+    qr = ob.rotary(ob.rms_norm(a_q, eps), f1[:E].detach().double().cpu(), f2[:E].detach().double().cpu())
+    (g,) = torch.autograd.grad(qr, a_q, dq.detach().double().cpu().permute(0, 2, 1, 3))
+    return rx.detach().double().cpu()[:, None, :E, None] * g.permute(0, 2, 1, 3)

@@ -101,14 +101,15 @@ def _bits(t):
     return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
 
 
-def _run_block(lib, g, f1, f2, w, tables_bf16, var=None):
+def _run_block(lib, g, f1, f2, w, tables_bf16, var=None, n_active=0, table_grad=True):
     """mea_fwd + mea_bwd (or their varlen forms with var = (cu, nseq, max_len))
-    with table gradients; workspaces guarded. Returns every output."""
+    with table gradients (NULL df1 / df2 without table_grad); workspaces
+    guarded. Returns every output."""
     B, T, C, H, N = w.B, w.T, w.C, w.H, w.N
     HN, M = H * N, B * T
     t_max = var[2] if var is not None else T
-    d = _lib.desc(B, T, C, H, N, t_max, 1e-6, 0, tables_bf16)
-    d_ws = _lib.desc(B, T, C, H, N, T, 1e-6, 0, tables_bf16)
+    d = _lib.desc(B, T, C, H, N, t_max, 1e-6, n_active, tables_bf16)
+    d_ws = _lib.desc(B, T, C, H, N, T, 1e-6, n_active, tables_bf16)
     s = _lib.stream_of(torch.device("cuda"))
     wts = [g[n].data_ptr() for n in ("wq", "wk", "wv", "wg", "wo")]
     y = torch.empty(M * C, dtype=torch.bfloat16, device="cuda")
@@ -124,14 +125,14 @@ def _run_block(lib, g, f1, f2, w, tables_bf16, var=None):
     rows = t_max
     dx = torch.empty(M * C, dtype=torch.bfloat16, device="cuda")
     dws = [torch.empty(HN * C, dtype=torch.bfloat16, device="cuda") for _ in range(5)]
-    df1 = torch.empty(rows * N, dtype=torch.float32, device="cuda")
-    df2 = torch.empty(rows * N, dtype=torch.float32, device="cuda")
-    nb = lib.mea_workspace_bytes(ctypes.byref(d_ws), _lib.MEA_PASS_BWD_TABLES)
+    df1 = torch.empty(rows * N, dtype=torch.float32, device="cuda") if table_grad else None
+    df2 = torch.empty(rows * N, dtype=torch.float32, device="cuda") if table_grad else None
+    nb = lib.mea_workspace_bytes(ctypes.byref(d_ws), _lib.MEA_PASS_BWD_TABLES if table_grad else _lib.MEA_PASS_BWD)
     wsb_buf, wsb = _ws_guarded(nb)
     bwd = lib.mea_bwd_varlen if var is not None else lib.mea_bwd
     rc = bwd(ctypes.byref(d), *head, g["dy"].data_ptr(), g["x"].data_ptr(), *wts, f1.data_ptr(), f2.data_ptr(),
-             o.data_ptr(), lse.data_ptr(), dx.data_ptr(), *(t.data_ptr() for t in dws), df1.data_ptr(),
-             df2.data_ptr(), wsb.data_ptr(), nb, s)
+             o.data_ptr(), lse.data_ptr(), dx.data_ptr(), *(t.data_ptr() for t in dws), _lib.ptr(df1),
+             _lib.ptr(df2), wsb.data_ptr(), nb, s)
     assert rc == 0, _lib.strerror(rc)
     torch.cuda.synchronize()
     assert _ws_intact(wsf_buf) and _ws_intact(wsb_buf), "write past the workspace"
@@ -171,3 +172,42 @@ def test_packed_bf16_tables_varlen_bitwise():
     packed = _run_block(lib, g, f1, f2, w, True, var)
     for k in plain:
         assert torch.equal(_bits(plain[k]), _bits(packed[k])), f"{k} differs with packed tables"
+
+
+@pytest.mark.parametrize("pad", ["identity", "zero"])
+@pytest.mark.parametrize("table_grad", [False, True], ids=["no-table-grad", "table-grad"])
+def test_narrow_heads_through_the_abi(pad, table_grad):
+    """Heads of 32 dimensions through the C ABI as the header describes them:
+    N = 64, N_active = 32, the last 32 rows of every head of Wq, Wk, Wv, Wg
+    and columns of Wo zero, and the padding columns of the rotary tables
+    holding identity pairs (f1 = 1, f2 = 0) or zeros. Both give the oracle's
+    N = 32 block (no NaN from the zero pair blocks in the backward)."""
+    from memory_efficient_attn_layer_amd.attention import _pad_heads
+
+    lib = _lib.load()
+    w = Workload(99, "n32", 2, 150, 256, 4, 32, 4.0, 64)
+    inp = make_inputs(w)
+    ref = ob.block_grads(inp, w.H, w.N)
+    g = {k: v.cuda().contiguous() for k, v in inp.items()}
+    wts, f1p, f2p = _pad_heads(w.H, w.N, [g[n] for n in ("wq", "wk", "wv", "wg", "wo")], g["f1"], g["f2"])
+    if pad == "zero":
+        f1p, f2p = f1p.clone(), f2p.clone()
+        f1p[:, w.N:] = 0
+    gp = dict(g, **{n: t.contiguous() for n, t in zip(("wq", "wk", "wv", "wg", "wo"), wts)})
+    wp = Workload(99, "n32p", w.B, w.T, w.C, w.H, 64)
+    out = _run_block(lib, gp, f1p[:w.T].float().contiguous(), f2p[:w.T].float().contiguous(), wp, False,
+                     n_active=w.N, table_grad=table_grad)
+    B, T, C, H, N = w.B, w.T, w.C, w.H, w.N
+    for k, v in out.items():
+        if v is not None:
+            assert torch.isfinite(v.float()).all(), f"{k}: non-finite values"
+    assert_out_close("y", out["y"].view(B, T, C), ref["y"])
+    assert_grad_close("dx", out["dx"].view(B, T, C), ref["dx"])
+    for k in ("dwq", "dwk", "dwv", "dwg"):
+        got = out[k].view(H, 64, C)
+        assert torch.all(got[:, N:] == 0), f"{k}: padding rows nonzero"
+        assert_grad_close(k, got[:, :N].reshape(H * N, C), ref[k])
+    assert_grad_close("dwo", out["dwo"].view(C, H, 64)[:, :, :N].reshape(C, H * N), ref["dwo"])
+    if table_grad:
+        assert_grad_close("df1", out["df1"].view(T, 64)[:, :N], ref["df1"][:T])
+        assert_grad_close("df2", out["df2"].view(T, 64)[:, :N], ref["df2"][:T])

@@ -147,6 +147,22 @@ def test_block_forward_backward(label, w, B):
     check_block(w, B=B)
 
 
+# The same block with tables that take no gradient (df1 = df2 = NULL), the
+# case of a module whose tables are buffers: the attention backward then runs
+# its other kernel forms (one head per workgroup, three workgroups per CU at
+# N = 64, the row tails' operands fetched in one round trip).
+BUFFER_TABLE_CASES = [c for c in BLOCK_CASES if c[0] in {
+    "cfg0-full", "cfg1-b1-t4096", "cfg2-yarn4-b1-t2048", "cfg3-b1-t1024", "ragged-b3-t77", "ragged-b2-t200-n128",
+    "t129-b1", "yarn8-b2-t300-n128", "h5-hn320-b1-t150", "c2048-h16-n128-yarn8-b1-t256", "n32-h8-c256-b2-t100",
+    "n16-h4-c64-b2-t70", "n256-h2-c512-b2-t130", "n256-yarn4-h3-c768-b1-t200", "n256-h1-c256-b1-t70"}]
+
+
+@pytest.mark.parametrize("label,w,B", BUFFER_TABLE_CASES, ids=[c[0] for c in BUFFER_TABLE_CASES])
+def test_block_forward_backward_buffer_tables(label, w, B):
+    got, _ = check_block(w, B=B, table_grad=False)
+    assert got["df1"] is None and got["df2"] is None
+
+
 @pytest.mark.parametrize("tscale", [2.0, 2.5], ids=["fixed-offset-wide-range", "online-fallback"])
 def test_block_logit_range(tscale):
     """Rotary tables scaled by tscale widen the logit range. The block bounds

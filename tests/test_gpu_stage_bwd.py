@@ -16,13 +16,22 @@ the same intermediates (oracle.block.block_grads(with_intermediates=True)):
   da_g   = rx * dL/da_g     (B, T, H*N)
   df1, df2 (T, N)                          the table gradients, per position
 
-Rows of queries with fewer than EARLY keys (t < EARLY) are held to
-EARLY_TOL instead of ROW_TOL for da_q: every flash backward (the
-reference's aten kernel included) forms delta from the bf16-rounded saved O,
-so sum_j dS_tj is not exactly 0 and dQ_t carries an error of about
-dO . (O - bf16(O)) times the mean key, which nothing averages away when a
-query sees two or three keys (tests/test_flash_numerics.py reproduces it on
-the CPU: 11% at such a row with bf16 operands, under 2% beyond t = 16).
+Rows t >= 16 of da_q are checked against the oracle. The first 16 query rows
+are checked against parity_util.early_daq_reference, at the same ROW_TOL:
+every flash backward (the reference's aten kernel included) forms delta from
+the bf16-rounded saved O, so sum_j dS_tj is not exactly 0 and dQ_t carries an
+error of about dO . (O - bf16(O)) times the mean key, which nothing averages
+away when a query sees two or three keys (12% against the oracle at such a
+row). That reference takes every operand as the kernel holds it (stored q,
+bf16 k and v, the kernel's dO and saved O), so the effect is in it too and a
+defect confined to the first query tile of a head (diagonal masking, tile-0
+indexing) still fails the row bound (tests/test_flash_numerics.py measures
+both on the CPU).
+
+Both forms of the attention-backward kernels run: without table gradients
+(df1 = df2 = NULL, the kernels a module with buffer tables runs: one head per
+workgroup) and with them (one workgroup walks every head of its block and
+writes per-token table partials).
 
 rx = 1/rms(x) per token. The chain da = rq (R^T dq - qh (R^T dq . qh) / N)
 is an invertible rotation followed by a projection that removes only the
@@ -35,12 +44,11 @@ import torch
 from memory_efficient_attn_layer_amd import stages
 from memory_efficient_attn_layer_amd.synthetic import WORKLOADS, Workload, make_inputs
 from oracle import block as ob
-from tests.parity_util import ROW_TOL, assert_grad_close, assert_rows_close
+from tests.parity_util import ROW_TOL, assert_grad_close, assert_rows_close, early_daq_reference
 
 pytestmark = pytest.mark.gpu
 
 EARLY = 16
-EARLY_TOL = 0.25
 
 W0, W1 = WORKLOADS[0], WORKLOADS[1]
 NAMES = ("x", "wq", "wk", "wv", "wg", "wo", "f1", "f2")
@@ -61,14 +69,16 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("table_grad", [False, True], ids=["no-table-grad", "table-grad"])
 @pytest.mark.parametrize("label,w,B", CASES, ids=[c[0] for c in CASES])
-def test_backward_intermediates_per_row(label, w, B):
-    print(f"\n[{label}] B={w.B if B is None else B} T={w.T} C={w.C} H={w.H} N={w.N} yarn={w.yarn_scale}", flush=True)
+def test_backward_intermediates_per_row(label, w, B, table_grad):
+    print(f"\n[{label}] B={w.B if B is None else B} T={w.T} C={w.C} H={w.H} N={w.N} yarn={w.yarn_scale} "
+          f"table_grad={table_grad}", flush=True)
     inp = make_inputs(w, B=B)
     g = {k: v.cuda() for k, v in inp.items()}
     H, N = w.H, w.N
     _, o_save, lse = stages.fwd_saved(*(g[n] for n in NAMES), H, N)
-    got = stages.bwd_grads(*(g[n] for n in NAMES), o_save, lse, g["dy"], H, N, table_grad=True)
+    got = stages.bwd_grads(*(g[n] for n in NAMES), o_save, lse, g["dy"], H, N, table_grad=table_grad)
     torch.cuda.synchronize()
 
     ref = ob.block_grads(inp, H, N, dtype=torch.float32, with_intermediates=True)
@@ -96,9 +106,13 @@ def test_backward_intermediates_per_row(label, w, B):
     e = min(EARLY, T)
     if T > e:
         assert_rows_close("da_q (dQ chain), t >= 16", got["daq"][:, :, e:], daq_ref[:, :, e:])
-    assert_rows_close("da_q (dQ chain), t < 16", got["daq"][:, :, :e], daq_ref[:, :, :e], tol=EARLY_TOL)
+    early = early_daq_reference(it, got["dO"], o_save, inp["f1"], inp["f2"], rx, H, N, e)
+    assert_rows_close("da_q (dQ chain), t < 16, kernel operands", got["daq"][:, :, :e], early)
     assert_rows_close("da_k (dK chain)", got["dak"], rx_h * head_major(ig["a_k"]))
     assert_rows_close("da_g", got["dag"], rx[:, :, None] * ig["a_g"])
+    if not table_grad:
+        assert "df1" not in got
+        return
     assert_grad_close("df1", got["df1"][:T], ref["df1"][:T])
     assert_grad_close("df2", got["df2"][:T], ref["df2"][:T])
     assert_rows_close("df1 per position", got["df1"][:T], ref["df1"][:T])

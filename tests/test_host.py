@@ -351,3 +351,26 @@ def test_bf16_table_flag_follows_table_dtype():
     vals = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
     finite = vals[torch.isfinite(vals)]
     assert torch.equal(finite.float().bfloat16().view(torch.int16), finite.view(torch.int16))
+
+
+def test_varlen_host_offsets_are_checked():
+    """fused_attn_varlen checks offsets it holds on the host (a list or a CPU
+    tensor) before any launch: a max_len below the longest sequence would
+    leave that sequence's last rows unwritten, so it is an error."""
+    from memory_efficient_attn_layer_amd.attention import check_offsets, fused_attn_varlen
+
+    m = CausalSoftmaxAttention(256, 4, 64)
+    yarn = Yarn(64, 512)
+    x = torch.randn(300, 256).bfloat16()
+    args = (x, m.q_proj, m.k_proj, m.v_proj, m.g_proj, m.o_proj, yarn, 4, 64)
+    with pytest.raises(ValueError, match="below the longest"):
+        fused_attn_varlen(*args, [0, 100, 300], max_len=150)
+    with pytest.raises(ValueError, match="below the longest"):
+        fused_attn_varlen(*args, torch.tensor([0, 100, 300], dtype=torch.int32), max_len=199)
+    with pytest.raises(ValueError, match="nondecreasing"):
+        fused_attn_varlen(*args, [0, 200, 100, 300])
+    with pytest.raises(ValueError, match="from 0 to 300"):
+        fused_attn_varlen(*args, [0, 100, 250])
+    with pytest.raises(ValueError, match="nseq"):
+        fused_attn_varlen(*args, [300])
+    assert check_offsets([0, 100, 100, 300], 300) == 200  # empty sequences are fine
