@@ -100,7 +100,9 @@ enum {
 
 /* Which pass a workspace size is asked for: the forward, the backward, or a
  * backward that also writes the table gradients df1 / df2 (it needs
- * B * T * N * 8 more bytes for per-token partial sums). */
+ * B * T * H * (2 * N + 8) more bytes: the gradient of the k projection beside
+ * k, which the table gradients read after the attention backward, and one
+ * fp32 dot product per (b, h, t) row of q and of k). */
 enum { MEA_PASS_FWD = 0, MEA_PASS_BWD = 1, MEA_PASS_BWD_TABLES = 2 };
 
 /*

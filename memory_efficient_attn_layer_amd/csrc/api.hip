@@ -24,7 +24,7 @@ struct Layout {
   size_t wpk;                                // k-slab-major copies of Wq, Wk, Wv, Wg
   size_t dO, daq, dag;                       // backward (da_k, da_v overwrite k, v)
   size_t rx, rq, rk, delta, woT, wcatT, part;
-  size_t tpart;                              // table-gradient partials (MEA_PASS_BWD_TABLES)
+  size_t dak, dotq, dotk;                    // table gradients (MEA_PASS_BWD_TABLES): da_k beside k, row dots
   size_t total;
 };
 
@@ -60,7 +60,13 @@ Layout make_layout(const mea_desc& d, int pass) {
     L.woT = take(HN * C * 2);
     L.wcatT = take(C * 4 * HN * 2);
     L.part = take((size_t)mea::dw_splits((int)M, (int)C, (int)HN) * (4 * HN * C + C * HN) * 4);
-    if (pass == MEA_PASS_BWD_TABLES) L.tpart = take(M * 2 * (size_t)d.N * 4);
+    if (pass == MEA_PASS_BWD_TABLES) {
+      // The table gradients read k after the dK/dV kernel: da_k gets its own
+      // rows, and the kernels leave one dot product per (b, h, t) row.
+      L.dak = take(act);
+      L.dotq = take(stat);
+      L.dotk = take(stat);
+    }
   }
   L.total = off;
   return L;
@@ -142,12 +148,12 @@ T* at(void* ws, size_t off) {
 enum KernelId {
   K_QKVG_PROJ, K_ATTN_FWD, K_GATE_OPROJ, K_TRANSPOSE, K_ZERO, K_DZ_GATE_BWD,
   K_ATTN_BWD_DQ, K_ATTN_BWD_DKDV, K_DW_PARTIAL, K_DW_REDUCE, K_DX,
-  K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_REDUCE, K_ROTARY_PACK, K_WEIGHT_PACK, K_COUNT
+  K_ATTN_DECODE, K_DECODE_COMBINE, K_SKINNY_GEMM, K_DECODE_PROJ, K_TABLE_GRAD, K_ROTARY_PACK, K_WEIGHT_PACK, K_COUNT
 };
 const char* const kKernelNames[K_COUNT] = {
     "qkvg_proj", "attn_fwd", "gate_oproj", "transpose", "zero_f32", "dz_gate_bwd",
     "attn_bwd_dq", "attn_bwd_dkdv", "dw_partial", "dw_reduce", "dx",
-    "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad_reduce", "rotary_pack", "weight_pack"};
+    "attn_decode", "attn_decode_combine", "skinny_gemm", "decode_proj", "table_grad", "rotary_pack", "weight_pack"};
 
 struct ProfRec {
   int kernel;
@@ -409,13 +415,15 @@ int fwd_impl(const mea_desc* d, const Varlen* var, const void* x, const void* wq
 
 // Buffers of one backward pass inside the workspace (and dx).
 struct BwdBufs {
-  bf16_bits *q, *k, *v, *sig, *dO, *daq, *dag, *woT, *wcatT;
+  bf16_bits *q, *k, *v, *sig, *dO, *daq, *dak, *dag, *woT, *wcatT;
   float *rx, *rq, *rk, *delta, *part;
+  float *dotq, *dotk;  // table gradients only, else null
   int ld_dag;
 };
 
-BwdBufs bwd_bufs(const mea_desc* d, void* ws, void* dag_ext, int ld_dag_ext) {
-  const Layout L = make_layout(*d, MEA_PASS_BWD);
+// tables: the backward also writes df1 / df2 (MEA_PASS_BWD_TABLES layout).
+BwdBufs bwd_bufs(const mea_desc* d, void* ws, void* dag_ext, int ld_dag_ext, bool tables) {
+  const Layout L = make_layout(*d, tables ? MEA_PASS_BWD_TABLES : MEA_PASS_BWD);
   BwdBufs b;
   b.q = at<bf16_bits>(ws, L.q);
   b.k = at<bf16_bits>(ws, L.k);
@@ -432,14 +440,19 @@ BwdBufs bwd_bufs(const mea_desc* d, void* ws, void* dag_ext, int ld_dag_ext) {
   b.rk = at<float>(ws, L.rk);
   b.delta = at<float>(ws, L.delta);
   b.part = at<float>(ws, L.part);
+  // da_k overwrites k (its last reader is the dK/dV kernel itself) unless
+  // the table gradients still need k.
+  b.dak = tables ? at<bf16_bits>(ws, L.dak) : b.k;
+  b.dotq = tables ? at<float>(ws, L.dotq) : nullptr;
+  b.dotk = tables ? at<float>(ws, L.dotk) : nullptr;
   return b;
 }
 
 // First half of the backward: weight transposes, the recompute of q, k, v,
 // sigmoid(g) and the RMS statistics, dZ with the gate backward, and the
-// attention backward with the exact q/k chain. Leaves the projection-output
-// gradients (rows scaled by rx) in bf.daq, bf.k (da_k), bf.v (da_v) and
-// bf.dag, and dO / delta in their buffers.
+// attention backward with the exact q/k chain, and the table gradients when
+// df1 is set. Leaves the projection-output gradients (rows scaled by rx) in
+// bf.daq, bf.dak, bf.v (da_v) and bf.dag, and dO / delta in their buffers.
 int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* x, const void* wq, const void* wk,
               const void* wv, const void* wg, const void* wo, const float* f1, const float* f2, const void* o_save,
               const float* lse_save, float* df1, float* df2, const BwdBufs& bf, void* ws, void* stream) {
@@ -501,10 +514,10 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
   ab.rq = bf.rq;
   ab.rk = bf.rk;
   ab.daq = bf.daq;
-  ab.dak = bf.k;
+  ab.dak = bf.dak;
   ab.dav = bf.v;
-  // Table gradients: per-token partials, summed over the sequences below.
-  ab.tpart = df1 != nullptr ? at<float>(ws, L.tpart) : nullptr;
+  ab.dotq = bf.dotq;
+  ab.dotk = bf.dotk;
   ab.B = (int)d->B;
   ab.H = H;
   ab.T = T;
@@ -518,9 +531,30 @@ int bwd_front(const mea_desc* d, const Varlen* var, const void* dy, const void* 
   MEA_TRY(timed(K_ATTN_BWD_DQ, s, [&] { return mea::launch_attn_bwd_dq(ab, N, s); }));
   MEA_TRY(timed(K_ATTN_BWD_DKDV, s, [&] { return mea::launch_attn_bwd_dkdv(ab, N, s); }));
   if (df1 != nullptr) {
+    mea::TableGradParams tg;
+    tg.q = bf.q;
+    tg.daq = bf.daq;
+    tg.k = bf.k;
+    tg.dak = bf.dak;
+    tg.dotq = bf.dotq;
+    tg.dotk = bf.dotk;
+    tg.rq = bf.rq;
+    tg.rk = bf.rk;
+    tg.rx = bf.rx;
+    tg.f1 = f1;
+    tg.f2 = f2;
+    tg.df1 = df1;
+    tg.df2 = df2;
+    tg.qscale = qs;
+    tg.inv_n = ab.inv_n;
+    tg.B = (int)d->B;
+    tg.H = H;
+    tg.T = T;
     // Table rows the block touches: positions 0 .. T-1 (packed: max_len - 1).
-    const int rows = var != nullptr ? var->max_len : T;
-    MEA_TRY(timed(K_TABLE_REDUCE, s, [&] { return mea::launch_table_grad_reduce(ab, N, rows, df1, df2, s); }));
+    tg.rows = var != nullptr ? var->max_len : T;
+    tg.cu = ab.cu;
+    tg.nseq = ab.nseq;
+    MEA_TRY(timed(K_TABLE_GRAD, s, [&] { return mea::launch_table_grad(tg, N, s); }));
   }
   return MEA_OK;
 }
@@ -568,10 +602,10 @@ int bwd_impl(const mea_desc* d, const Varlen* var, const void* dy, const void* x
   // workgroup reads the da_g rows it later overwrites, and nothing else
   // reads them after the weight gradients).
   const bool dag_in_dx = HN <= C && C <= 1024;
-  const BwdBufs bf = bwd_bufs(d, ws, dag_in_dx ? dx : nullptr, C);
+  const BwdBufs bf = bwd_bufs(d, ws, dag_in_dx ? dx : nullptr, C, df1 != nullptr);
   rc = bwd_front(d, var, dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, df1, df2, bf, ws, stream);
   if (rc != MEA_OK) return rc;
-  const mea::DaParts da = {bf.daq, bf.k, bf.v, bf.dag, bf.ld_dag, (int)d->B, T, H, N};
+  const mea::DaParts da = {bf.daq, bf.dak, bf.v, bf.dag, bf.ld_dag, (int)d->B, T, H, N};
 
   mea::DwParams dw;
   dw.da = da;
@@ -660,13 +694,13 @@ int mea_bwd_stage_grads(const mea_desc* d, const void* dy, const void* x, const 
   if (ws_bytes < L.total) return MEA_ERR_WORKSPACE;
   const int HN = (int)(d->H * d->N);
   // da_g goes straight to the caller's buffer (token-major rows of H*N).
-  const BwdBufs bf = bwd_bufs(d, ws, dag, HN);
+  const BwdBufs bf = bwd_bufs(d, ws, dag, HN, df1 != nullptr);
   rc = bwd_front(d, nullptr, dy, x, wq, wk, wv, wg, wo, f1, f2, o_save, lse_save, df1, df2, bf, ws, stream);
   if (rc != MEA_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t act = (size_t)(d->B * d->T) * (size_t)HN * 2, stat = (size_t)(d->B * d->H * d->T) * 4;
   MEA_TRY(hipMemcpyAsync(daq, bf.daq, act, hipMemcpyDeviceToDevice, s));
-  MEA_TRY(hipMemcpyAsync(dak, bf.k, act, hipMemcpyDeviceToDevice, s));
+  MEA_TRY(hipMemcpyAsync(dak, bf.dak, act, hipMemcpyDeviceToDevice, s));
   MEA_TRY(hipMemcpyAsync(dav, bf.v, act, hipMemcpyDeviceToDevice, s));
   MEA_TRY(hipMemcpyAsync(dO, bf.dO, act, hipMemcpyDeviceToDevice, s));
   MEA_TRY(hipMemcpyAsync(delta, bf.delta, stat, hipMemcpyDeviceToDevice, s));

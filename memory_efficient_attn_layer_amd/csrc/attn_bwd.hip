@@ -9,10 +9,14 @@
 //   q = R qh with R the per-pair block [[f1[2i], f2[2i]], [f2[2i+1], f1[2i+1]]]
 //   dqh = R^T dq
 //   da_q = rq * (dqh - qh * (dqh . qh) / N)
-//   dF1[t, n] += dq[n] qh[n],  dF2[t, n] += dq[n] qh[n^1]   (summed over
-//   batch and heads: per-token partials, then a reduce over sequences)
 // qh is recovered from the stored rotated q by inverting R per pair, so the
 // recompute pass does not have to keep the pre-rotation values.
+// Table gradients (fast_triton_attn.py:622-639), when asked for:
+//   dF1[t, n] = sum over batch and heads of dq[n] qh[n] + dk[n] kh[n],
+//   dF2[t, n] likewise with qh[n^1], kh[n^1]
+// come from table_grad_kernel after both kernels: it rebuilds dq and dk from
+// the stored da_q, da_k, q, k and the per-row dot products (dqh . qh) the
+// kernels leave, and sums over batch and heads in a fixed order.
 //
 // Two kernels (deterministic, no atomics on dQ):
 //   dq kernel   : one workgroup per (b, h, 4 waves of queries), streams key
@@ -39,20 +43,17 @@ namespace mea {
 // scaled by rx[tok_row0 + t]. out may be xrot itself: every lane writes only
 // the 16 bytes it has read, after reading them, and rows past T are not
 // written.
-// TG (rotary rows): the table-gradient products of the row go to
-// p.tpart[tok_row0 + t]: written when tg_first, else added. The same lane
-// handles the same 8 columns of a row in every call, so the read-modify-write
-// needs no synchronisation across calls of one workgroup.
-template <int N, bool TG = false>
+// dot_out (rotary rows, or null): row t's dot product dqh . qh goes to
+// dot_out[head_row0 + t] (the table gradients rebuild dq from it).
+template <int N>
 __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, const AttnBwdParams& p, int T,
                                              size_t tok_row0, size_t head_row0, bool rotary,
                                              const bf16_bits* xrot, float xscale, const float* rstat,
-                                             bf16_bits* out, bool tg_first = false) {
+                                             bf16_bits* out, float* dot_out) {
   constexpr int CPR = N / 8, RPP = 64 / CPR;
   // Passes, and passes whose global operands are fetched together (N = 64:
-  // all four, one memory round trip per call; the table-gradient variant
-  // would spill).
-  constexpr int NP = 32 / RPP, PB = N == 64 && !TG ? NP : 2;
+  // all four, one memory round trip per call).
+  constexpr int NP = 32 / RPP, PB = N == 64 ? NP : 2;
   static_assert(NP % PB == 0, "pass batches");
   const int lane = threadIdx.x & 63;
 #pragma unroll 1
@@ -129,30 +130,9 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
         const float sc = rxv * rr, cf = dot * p.inv_n;
 #pragma unroll
         for (int i = 0; i < 8; ++i) res[i] = sc * (dh[i] - xh[i] * cf);
-        if (TG && valid) {
-          float* d1 = p.tpart + (tok_row0 + t) * (2 * N) + dc * 8;
-          float* d2 = d1 + N;
-          f32x4 u[2], w[2];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            u[0][e] = dv[e] * xh[e];
-            u[1][e] = dv[4 + e] * xh[4 + e];
-            w[0][e] = dv[e] * xh[e ^ 1];
-            w[1][e] = dv[4 + e] * xh[(4 + e) ^ 1];
-          }
-          if (!tg_first) {
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-              u[hf] += *reinterpret_cast<const f32x4*>(d1 + 4 * hf);
-              w[hf] += *reinterpret_cast<const f32x4*>(d2 + 4 * hf);
-            }
-          }
-#pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            *reinterpret_cast<f32x4*>(d1 + 4 * hf) = u[hf];
-            *reinterpret_cast<f32x4*>(d2 + 4 * hf) = w[hf];
-          }
-        }
+        // Every lane of the row holds the same sum (a butterfly of commutative
+        // adds), so all of them store it: no lane test, no extra register.
+        if (dot_out != nullptr && valid) dot_out[head_row0 + t] = dot;
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) res[i] = rxv * dv[i];
@@ -183,8 +163,8 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // For N = 64 three workgroups share a CU (164 registers): 64 queries per wave
 // (two blocks sharing every K/V fragment) held two per SIMD ran 4.4% slower.
 // ---------------------------------------------------------------------------
-template <int N, bool VARLEN, bool TG>
-__global__ __launch_bounds__(256, N == 64 && !TG ? 3 : N == 256 ? 1 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
+template <int N, bool VARLEN>
+__global__ __launch_bounds__(256, N == 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   constexpr int QW = 32;                 // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
   constexpr int BQ = 4 * QW;             // queries per workgroup
@@ -202,16 +182,14 @@ __global__ __launch_bounds__(256, N == 64 && !TG ? 3 : N == 256 ? 1 : 2) void at
 
   // Each XCD walks whole heads (heaviest query block first), so the K/V
   // tiles of a head are fetched once into that XCD's L2. VARLEN: packed
-  // sequences (p.cu), rows relative to the sequence's first token. TG: a
-  // workgroup covers every head of its (sequence, query block), one after
-  // the other, so each token's table-gradient row has a single writer.
+  // sequences (p.cu), rows relative to the sequence's first token.
   int T, qi, b, h_first;
   size_t hrow_base, hrow_step, tok_row0;  // head hd's rows start at hrow_base + hd * hrow_step
-  const int nh = TG ? 1 : p.H;            // heads per grid row
+  const int nh = p.H;                     // heads per grid row
   if constexpr (!VARLEN) {
     T = p.T;
     const int nqb = (T + BQ - 1) / BQ;
-    const int lid = xcd_remap(blockIdx.x, p.B * nh * nqb);
+    const int lid = attn_item(blockIdx.x, p.B * nh * nqb, nqb);
     const int bh = lid / nqb;
     qi = nqb - 1 - lid % nqb;
     b = bh / nh;
@@ -234,8 +212,8 @@ __global__ __launch_bounds__(256, N == 64 && !TG ? 3 : N == 256 ? 1 : 2) void at
     tok_row0 = (size_t)start;
     if (qi * BQ >= T) return;  // past this sequence's end: uniform, before any barrier
   }
-  const int h_end = TG ? p.H : h_first + 1;
-  for (int hd = h_first; hd < h_end; ++hd) {
+  {
+    const int hd = h_first;
     const size_t head_row0 = hrow_base + (size_t)hd * hrow_step;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -407,9 +385,8 @@ __global__ __launch_bounds__(256, N == 64 && !TG ? 3 : N == 256 ? 1 : 2) void at
     __syncthreads();
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
-      head_row_bwd<N, TG>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, T, tok_row0, head_row0, true, p.q,
-                          1.0f / p.qscale, p.rq, p.daq, hd == 0);
-    if (TG) __syncthreads();  // the next head's statistics and tiles reuse the staging area
+      head_row_bwd<N>(stg + 32 * qb * FP, FP, q0w + 32 * qb, p, T, tok_row0, head_row0, true, p.q,
+                      1.0f / p.qscale, p.rq, p.daq, p.dotq);
   }
 }
 
@@ -440,8 +417,8 @@ __global__ __launch_bounds__(256, N == 64 && !TG ? 3 : N == 256 ? 1 : 2) void at
 // gradients, whose extra state would spill at 256 registers) runs one wave
 // per SIMD.
 // ---------------------------------------------------------------------------
-template <int N, bool VARLEN, bool TG>
-__global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : N == 128 && !TG ? 2 : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
+template <int N, bool VARLEN>
+__global__ __launch_bounds__(256, N == 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
   constexpr int KW = 32;                 // keys per wave
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
   static_assert(KB == 1, "one 32-key block per wave");
@@ -465,16 +442,14 @@ __global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : N == 128 && !TG ? 2 :
 
   // Each XCD walks whole heads, the key block that sees the most queries
   // first, so the Q/dO tiles of a head are shared in one L2. VARLEN: packed
-  // sequences (p.cu), rows relative to the sequence's first token. TG: a
-  // workgroup covers every head of its (sequence, key block), one after the
-  // other (each token's table-gradient row has a single writer).
+  // sequences (p.cu), rows relative to the sequence's first token.
   int T, ki, b, h_first;
   size_t hrow_base, hrow_step, tok_row0;  // head hd's rows start at hrow_base + hd * hrow_step
-  const int nh = TG ? 1 : p.H;            // heads per grid row
+  const int nh = p.H;                     // heads per grid row
   if constexpr (!VARLEN) {
     T = p.T;
     const int nkb = (T + BKV - 1) / BKV;
-    const int lid = xcd_remap(blockIdx.x, p.B * nh * nkb);
+    const int lid = attn_item(blockIdx.x, p.B * nh * nkb, nkb);
     const int bh = lid / nkb;
     ki = lid % nkb;
     b = bh / nh;
@@ -497,8 +472,8 @@ __global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : N == 128 && !TG ? 2 :
     tok_row0 = (size_t)start;
     if (ki * BKV >= T) return;  // past this sequence's end: uniform, before any barrier
   }
-  const int h_end = TG ? p.H : h_first + 1;
-  for (int hd = h_first; hd < h_end; ++hd) {
+  {
+    const int hd = h_first;
     const size_t head_row0 = hrow_base + (size_t)hd * hrow_step;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = lane & 31, h = lane >> 5;
@@ -668,7 +643,8 @@ __global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : N == 128 && !TG ? 2 :
           *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v;
         }
       __syncthreads();
-      head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, false, nullptr, 1.0f, nullptr, p.dav);
+      head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, false, nullptr, 1.0f, nullptr, p.dav,
+                      nullptr);
       __syncthreads();
 #pragma unroll
       for (int db = 0; db < DB; ++db)
@@ -678,47 +654,40 @@ __global__ __launch_bounds__(256, N == 64 ? (TG ? 2 : 3) : N == 128 && !TG ? 2 :
           *reinterpret_cast<f32x4*>(stg + c * FP + 32 * db + 8 * r4 + 4 * h) = v * (p.scale / p.qscale);
         }
       __syncthreads();
-      head_row_bwd<N, TG>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, true, p.k, 1.0f, p.rk, p.dak, false);
+      head_row_bwd<N>(stg, FP, kw0 + 32 * kb, p, T, tok_row0, head_row0, true, p.k, 1.0f, p.rk, p.dak, p.dotk);
       __syncthreads();
     }
   }
 }
 
-template <int N, bool VAR, bool TG>
+template <int N, bool VAR>
 struct DqKernel {
   static void launch(const AttnBwdParams& p, int G, hipStream_t s) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<N, VAR, TG>), dim3(G), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<N, VAR>), dim3(G), dim3(256), 0, s, p);
   }
 };
-template <int N, bool VAR, bool TG>
+template <int N, bool VAR>
 struct DkdvKernel {
   static void launch(const AttnBwdParams& p, int G, hipStream_t s) {
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<N, VAR, TG>), dim3(G), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<N, VAR>), dim3(G), dim3(256), 0, s, p);
   }
 };
 
-template <template <int, bool, bool> class K>
+template <template <int, bool> class K>
 static hipError_t launch_bwd_variant(const AttnBwdParams& p, int N, int blocks_per_seq, hipStream_t s) {
   if (p.sl2e != 1.0f) return hipErrorInvalidValue;  // stored q must be in log2 units
-  const bool var = p.cu != nullptr, tg = p.tpart != nullptr;
-  // Grid: (sequence, head, block); with table partials a workgroup walks
-  // every head of its (sequence, block).
-  const int G = (var ? p.nseq : p.B) * (tg ? 1 : p.H) * blocks_per_seq;
+  const bool var = p.cu != nullptr;
+  // Grid: (sequence, head, block).
+  const int G = (var ? p.nseq : p.B) * p.H * blocks_per_seq;
   if (G <= 0) return hipSuccess;
-  const int v = (N == 128 ? 4 : N == 256 ? 8 : 0) | (var ? 2 : 0) | (tg ? 1 : 0);
+  const int v = (N == 128 ? 2 : N == 256 ? 4 : 0) | (var ? 1 : 0);
   switch (v) {
-    case 0: K<64, false, false>::launch(p, G, s); break;
-    case 1: K<64, false, true>::launch(p, G, s); break;
-    case 2: K<64, true, false>::launch(p, G, s); break;
-    case 3: K<64, true, true>::launch(p, G, s); break;
-    case 4: K<128, false, false>::launch(p, G, s); break;
-    case 5: K<128, false, true>::launch(p, G, s); break;
-    case 6: K<128, true, false>::launch(p, G, s); break;
-    case 7: K<128, true, true>::launch(p, G, s); break;
-    case 8: K<256, false, false>::launch(p, G, s); break;
-    case 9: K<256, false, true>::launch(p, G, s); break;
-    case 10: K<256, true, false>::launch(p, G, s); break;
-    default: K<256, true, true>::launch(p, G, s); break;
+    case 0: K<64, false>::launch(p, G, s); break;
+    case 1: K<64, true>::launch(p, G, s); break;
+    case 2: K<128, false>::launch(p, G, s); break;
+    case 3: K<128, true>::launch(p, G, s); break;
+    case 4: K<256, false>::launch(p, G, s); break;
+    default: K<256, true>::launch(p, G, s); break;
   }
   return hipGetLastError();
 }
@@ -733,36 +702,143 @@ hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s) {
   return launch_bwd_variant<DkdvKernel>(p, N, (len + BKV - 1) / BKV, s);
 }
 
-// dF1 / dF2 from the per-token partials: one thread per 4 columns of one
-// position t, summing the rows of position t of every sequence that reaches
-// it, sequence after sequence (a fixed order: the result is deterministic).
-__global__ __launch_bounds__(256) void table_grad_reduce_kernel(const float* tpart, const int* cu, int nseq,
-                                                                int B, int T, int N, int rows, float* df1,
-                                                                float* df2) {
-  const int q = N / 2;  // 4-column groups per position (2N columns)
-  const int id = blockIdx.x * 256 + threadIdx.x;
-  if (id >= rows * q) return;
-  const int t = id / q, j = (id - t * q) * 4;
-  f32x4 acc = zero4();
-  if (cu == nullptr) {
-    for (int b = 0; b < B; ++b) acc += *reinterpret_cast<const f32x4*>(tpart + ((size_t)b * T + t) * (2 * N) + j);
-  } else {
-    for (int sq = 0; sq < nseq; ++sq) {
-      const int start = min(max(cu[sq], 0), T);
-      const int len = min(max(cu[sq + 1], start), T) - start;
-      if (t < len) acc += *reinterpret_cast<const f32x4*>(tpart + ((size_t)start + t) * (2 * N) + j);
+// ---------------------------------------------------------------------------
+// Table gradients (fast_triton_attn.py:622-639):
+//   dF1[t, n] = sum_{b, h} dq[n] qh[n] + dk[n] kh[n]
+//   dF2[t, n] = sum_{b, h} dq[n] qh[n^1] + dk[n] kh[n^1]
+// with dq, dk the gradients of the rotated q, k rows and qh, kh the rows
+// before the rotary. Neither dq nor qh is stored: per row, with R the rotary
+// pair blocks of position t, r = rx * rq and s = dqh . qh (left by the dQ
+// kernel in p.dotq),
+//   qh  = R^-1 q                       (q as stored, over qscale)
+//   dqh = da_q / r + qh * s / N        (the head RMSNorm backward, inverted)
+//   dq  = R^-T dqh
+// and likewise for k (p.dotk, da_k). da_q and da_k are the bf16 gradients the
+// weight and input gradients use, so dF sees the same rounding they do.
+// One workgroup covers PT positions: its threads take (slice, position,
+// 8-column chunk), each slice walks every SL-th (sequence, head) pair, and
+// the slices' sums meet in LDS in a fixed order (deterministic). Packed
+// sequences: position t of sequence s is token cu[s] + t, skipped where
+// the sequence is shorter.
+// ---------------------------------------------------------------------------
+template <int N>
+__global__ __launch_bounds__(256) void table_grad_kernel(TableGradParams p) {
+  constexpr int CPR = N / 8, PT = 4, SL = 256 / (CPR * PT);
+  __shared__ __attribute__((aligned(16))) float red[SL][PT][2 * N];
+  const int tid = threadIdx.x;
+  const int dc = tid % CPR, pp = (tid / CPR) % PT, sl = tid / (CPR * PT);
+  const int t = blockIdx.x * PT + pp;
+  const bool live = t < p.rows;
+  const int tc = live ? t : p.rows - 1;
+  float a1[8], a2[8], inv[4];
+  {
+    const float* f1r = p.f1 + (size_t)tc * N + dc * 8;
+    const float* f2r = p.f2 + (size_t)tc * N + dc * 8;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const f32x4 u = *reinterpret_cast<const f32x4*>(f1r + 4 * hf);
+      const f32x4 w = *reinterpret_cast<const f32x4*>(f2r + 4 * hf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a1[4 * hf + e] = u[e];
+        a2[4 * hf + e] = w[e];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const float det = a1[i] * a1[i + 1] - a2[i] * a2[i + 1];
+      inv[i / 2] = det != 0.f ? __builtin_amdgcn_rcpf(det) : 0.f;  // zero pair block: zero rows
     }
   }
-  float* dst = j < N ? df1 + (size_t)t * N + j : df2 + (size_t)t * N + (j - N);
-  *reinterpret_cast<f32x4*>(dst) = acc;
+  float u[8], w[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) u[e] = w[e] = 0.f;
+
+  // One row's contribution: x as stored (times xscale), its da, r = rx * rr
+  // and the dot product s.
+  auto add_row = [&](const u32x4& xw, const u32x4& daw, float xscale, float r_inv, float sdot) {
+    float xv[8], da[8], xh[8], dh[8];
+    unpack8(xw, xv);
+    unpack8(daw, da);
+    const float cf = sdot * p.inv_n;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const float x0 = xv[i] * xscale, x1 = xv[i + 1] * xscale;
+      xh[i] = (a1[i + 1] * x0 - a2[i] * x1) * inv[i / 2];
+      xh[i + 1] = (a1[i] * x1 - a2[i + 1] * x0) * inv[i / 2];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dh[i] = da[i] * r_inv + xh[i] * cf;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const float d0 = (a1[i + 1] * dh[i] - a2[i + 1] * dh[i + 1]) * inv[i / 2];
+      const float d1 = (a1[i] * dh[i + 1] - a2[i] * dh[i]) * inv[i / 2];
+      u[i] += d0 * xh[i];
+      u[i + 1] += d1 * xh[i + 1];
+      w[i] += d0 * xh[i + 1];
+      w[i + 1] += d1 * xh[i];
+    }
+  };
+
+  const bool var = p.cu != nullptr;
+  const int nbh = (var ? p.nseq : p.B) * p.H;
+  if (live) {
+#pragma unroll 2
+    for (int i = sl; i < nbh; i += SL) {
+      const int b = i / p.H, h = i - b * p.H;
+      size_t row, tok;
+      if (!var) {
+        row = ((size_t)b * p.H + h) * p.T + t;
+        tok = (size_t)b * p.T + t;
+      } else {
+        // Offsets clamped to [0, total], as in the attention kernels.
+        const int start = min(max(p.cu[b], 0), p.T);
+        const int len = min(max(p.cu[b + 1], start), p.T) - start;
+        if (t >= len) continue;
+        row = (size_t)h * p.T + start + t;
+        tok = (size_t)start + t;
+      }
+      const u32x4 qw = ld16(p.q + row * N + dc * 8), daqw = ld16(p.daq + row * N + dc * 8);
+      const u32x4 kw = ld16(p.k + row * N + dc * 8), dakw = ld16(p.dak + row * N + dc * 8);
+      const float rxv = p.rx[tok];
+      const float rq = p.rq[row], rk = p.rk[row], sq = p.dotq[row], sk = p.dotk[row];
+      add_row(qw, daqw, 1.0f / p.qscale, __builtin_amdgcn_rcpf(rxv * rq), sq);
+      add_row(kw, dakw, 1.0f, __builtin_amdgcn_rcpf(rxv * rk), sk);
+    }
+  }
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    *reinterpret_cast<f32x4*>(&red[sl][pp][dc * 8 + 4 * hf]) = f32x4{u[4 * hf], u[4 * hf + 1], u[4 * hf + 2], u[4 * hf + 3]};
+    *reinterpret_cast<f32x4*>(&red[sl][pp][N + dc * 8 + 4 * hf]) =
+        f32x4{w[4 * hf], w[4 * hf + 1], w[4 * hf + 2], w[4 * hf + 3]};
+  }
+  __syncthreads();
+  if (sl == 0 && live) {
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      f32x4 s1 = *reinterpret_cast<const f32x4*>(&red[0][pp][dc * 8 + 4 * hf]);
+      f32x4 s2 = *reinterpret_cast<const f32x4*>(&red[0][pp][N + dc * 8 + 4 * hf]);
+#pragma unroll
+      for (int k = 1; k < SL; ++k) {
+        s1 += *reinterpret_cast<const f32x4*>(&red[k][pp][dc * 8 + 4 * hf]);
+        s2 += *reinterpret_cast<const f32x4*>(&red[k][pp][N + dc * 8 + 4 * hf]);
+      }
+      *reinterpret_cast<f32x4*>(p.df1 + (size_t)t * N + dc * 8 + 4 * hf) = s1;
+      *reinterpret_cast<f32x4*>(p.df2 + (size_t)t * N + dc * 8 + 4 * hf) = s2;
+    }
+  }
 }
 
-hipError_t launch_table_grad_reduce(const AttnBwdParams& p, int N, int rows, float* df1, float* df2,
-                                    hipStream_t s) {
-  const int n = rows * (N / 2);
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(table_grad_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p.tpart, p.cu, p.nseq, p.B,
-                     p.T, N, rows, df1, df2);
+hipError_t launch_table_grad(const TableGradParams& p, int N, hipStream_t s) {
+  constexpr int PT = 4;
+  if (p.rows <= 0) return hipSuccess;
+  const dim3 grid((p.rows + PT - 1) / PT);
+  if (N == 64)
+    hipLaunchKernelGGL(table_grad_kernel<64>, grid, dim3(256), 0, s, p);
+  else if (N == 128)
+    hipLaunchKernelGGL(table_grad_kernel<128>, grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(table_grad_kernel<256>, grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -79,14 +79,10 @@ struct AttnBwdParams {
   // by rx. dak / dav may be k / v themselves: the dK/dV kernel reads only
   // its own key rows of k and v, each before writing them.
   bf16_bits *daq, *dak, *dav;
-  // Table-gradient partials (M, 2N) fp32, or null. Row m (a token) gets the
-  // sum over heads of dq*qh (columns 0..N-1) and dq*qh[n^1] (N..2N-1) from
-  // the dQ kernel, which writes it, plus dk*kh and dk*kh[n^1] from the dK/dV
-  // kernel, which adds; launch_table_grad_reduce sums the rows of one
-  // position over the sequences into dF1, dF2. With tpart set, one
-  // workgroup covers every head of its (sequence, row block), so each row
-  // has a single writer and the sums have a fixed order.
-  float* tpart;
+  // Per-row dot products dqh . qh and dkh . kh of the head RMSNorm backward,
+  // (B, H, T) fp32, written when non-null (table gradients; then dak must
+  // not be k, which table_grad_kernel reads afterwards).
+  float *dotq, *dotk;
   int B, H, T;
   float scale;                              // softmax scale 1/sqrt(N)
   float sl2e;                               // must be 1: stored q . k is in log2 units
@@ -97,10 +93,21 @@ struct AttnBwdParams {
 };
 hipError_t launch_attn_bwd_dq(const AttnBwdParams& p, int N, hipStream_t s);
 hipError_t launch_attn_bwd_dkdv(const AttnBwdParams& p, int N, hipStream_t s);
-// dF1[t] = sum over sequences of tpart[first row + t][0..N), dF2 from columns
-// N..2N, for rows t < rows (sequences shorter than t + 1 contribute nothing).
-hipError_t launch_table_grad_reduce(const AttnBwdParams& p, int N, int rows, float* df1, float* df2,
-                                    hipStream_t s);
+// dF1 / dF2 (rows, N) fp32 from the stored q, k, their gradients da_q,
+// da_k and the per-row dot products of the attention backward, summed over
+// batch (or packed sequences) and heads in a fixed order.
+struct TableGradParams {
+  const bf16_bits *q, *daq, *k, *dak;       // (B, H, T, N) head-major; q as stored (times qscale)
+  const float *dotq, *dotk, *rq, *rk;       // (B, H, T)
+  const float* rx;                          // (M)
+  const float *f1, *f2;                     // (rows, N) fp32 tables
+  float *df1, *df2;                         // (rows, N) out
+  float qscale, inv_n;
+  int B, H, T, rows;
+  const int* cu;                            // packed sequences (B = 1, T = total tokens) or null
+  int nseq;
+};
+hipError_t launch_table_grad(const TableGradParams& p, int N, hipStream_t s);
 
 // y = (o * sig) Wo^T.
 struct OprojParams {
