@@ -32,7 +32,7 @@
  *
  * Supported shapes: N in {64, 128, 256} (heads of 16 or 32 dimensions
  * zero-padded to N = 64, see N_active);
- * C a multiple of 32, 32 <= C <= 4096; H >= 1;
+ * C a multiple of 32, 32 <= C <= 16384, with H * N * C < 2^29; H >= 1;
  * B, T >= 1; T <= T_max; and
  * for the backward H * (T + 256) * N < 2^30 (one batch's head-major gradient
  * rows are addressed with 32-bit byte offsets).

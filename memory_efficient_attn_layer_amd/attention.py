@@ -34,8 +34,9 @@ from . import _lib
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 PADDED_HEAD_DIMS = (16, 32)  # carried zero-padded to PAD_N dimensions
 PAD_N = 64
-MAX_C_FORWARD = 4096
-MAX_C_BACKWARD = 4096
+MAX_C_FORWARD = 16384
+MAX_C_BACKWARD = 16384
+MAX_HN_C = 1 << 29  # H * N * C below this: 32-bit element indices into the stacked weights
 
 
 def _validate(x, weights, factor1, factor2, H: int, N: int, eps: float, need_backward: bool) -> None:
@@ -55,6 +56,8 @@ def _validate(x, weights, factor1, factor2, H: int, N: int, eps: float, need_bac
     if need_backward and C > MAX_C_BACKWARD:
         raise ValueError(f"backward supports C <= {MAX_C_BACKWARD}, got C={C}")
     HN = H * N
+    if HN * C >= MAX_HN_C:
+        raise ValueError(f"H*N*C = {HN * C} must be below 2^29")
     names = ("q_proj", "k_proj", "v_proj", "g_proj", "o_proj")
     shapes = ((HN, C),) * 4 + ((C, HN),)
     for name, w, shp in zip(names, weights, shapes):

@@ -72,6 +72,11 @@ Layout make_layout(const mea_desc& d, int pass) {
   return L;
 }
 
+// Widest model: the kernels walk C in 32-wide k-slabs and 1024-wide feature
+// groups, so any multiple of 32 works; the cap keeps every 32-bit slab and
+// row offset far from overflow.
+constexpr int64_t kMaxC = 16384;
+
 int validate(const mea_desc* d, int pass) {
   if (d == nullptr) return MEA_ERR_NULL;
   if (d->B < 1 || d->T < 1 || d->H < 1 || d->T_max < d->T) return MEA_ERR_SHAPE;
@@ -80,13 +85,16 @@ int validate(const mea_desc* d, int pass) {
     return MEA_ERR_HEAD_DIM;
   if (d->C < 32 || d->C % 32 != 0) return MEA_ERR_MODEL_DIM;
   const bool bwd = pass == MEA_PASS_BWD || pass == MEA_PASS_BWD_TABLES;
-  if (d->C > 4096) return MEA_ERR_MODEL_DIM;
+  if (d->C > kMaxC) return MEA_ERR_MODEL_DIM;
   if (!(d->eps > 0.f) || !isfinite(d->eps)) return MEA_ERR_EPS;
   // All row and element indices used by the kernels fit in 31 bits.
   const int64_t M = d->B * d->T, HN = d->H * d->N;
   if (M >= (INT64_C(1) << 31) || HN >= 65536 || d->B * d->H * d->T >= (INT64_C(1) << 31) ||
       d->T_max * d->N >= (INT64_C(1) << 31))
     return MEA_ERR_SHAPE;
+  // Element indices into the four stacked weight matrices (4 * H*N * C) are
+  // 32-bit.
+  if (HN * d->C >= (INT64_C(1) << 29)) return MEA_ERR_MODEL_DIM;
   // The backward GEMMs address a head-major gradient with 32-bit byte
   // offsets spanning up to one head of one batch plus a few hundred rows.
   if (bwd && d->H * (d->T + 256) * d->N >= (INT64_C(1) << 30)) return MEA_ERR_SHAPE;
@@ -924,7 +932,7 @@ const char* mea_strerror(int code) {
     case MEA_ERR_NULL: return "a required pointer is NULL (or only one of a pair was given)";
     case MEA_ERR_SHAPE: return "B, T, H must be >= 1, T <= T_max, and indices must fit 31 bits";
     case MEA_ERR_HEAD_DIM: return "head width N must be 64, 128 or 256";
-    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 32 in [32, 4096]";
+    case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 32 in [32, 16384] with H*N*C < 2^29";
     case MEA_ERR_WORKSPACE: return "workspace smaller than mea_workspace_bytes()";
     case MEA_ERR_ALIGN: return "a pointer is not 16-byte aligned";
     case MEA_ERR_EPS: return "eps must be finite and positive";

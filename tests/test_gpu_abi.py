@@ -32,7 +32,8 @@ def _intact(buf):
 
 
 CASES = [Workload(99, "ragged", 3, 77, 256, 2, 64), Workload(99, "n128", 2, 200, 512, 4, 128),
-         Workload(99, "c1024", 1, 130, 1024, 8, 64), Workload(99, "c2048", 1, 96, 2048, 16, 128)]
+         Workload(99, "c1024", 1, 130, 1024, 8, 64), Workload(99, "c2048", 1, 96, 2048, 16, 128),
+         Workload(99, "c8192", 1, 40, 8192, 8, 128)]
 
 
 @pytest.mark.parametrize("w", CASES, ids=[f"B{w.B}-T{w.T}-C{w.C}-H{w.H}-N{w.N}" for w in CASES])

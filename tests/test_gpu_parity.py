@@ -33,6 +33,7 @@ STAGE_CASES = [
     # 512-feature groups.
     ("c1280-h4-b1-t64", _w("c1280", 1, 64, 1280, 4, 64), None),
     ("c2048-h8-n128-b1-t64", _w("c2048", 1, 64, 2048, 8, 128), None),
+    ("c16384-h4-n128-b1-t32", _w("c16384", 1, 32, 16384, 4, 128), None),
 ]
 
 
@@ -107,8 +108,13 @@ BLOCK_CASES = [
     ("c1280-h5-b2-t100", _w("c1280", 2, 100, 1280, 5, 64), None),
     ("c2048-h16-n128-yarn8-b1-t256", _w("c2048", 1, 256, 2048, 16, 128, 8.0, 64), None),
     ("c3072-h4-b1-t64", _w("c3072", 1, 64, 3072, 4, 64), None),
-    # The widest model the library accepts (four dx feature groups; C > H*N).
+    # Wide models: dx walks 4, 5, 8 and 16 feature groups of 1024 (C > H*N
+    # and C = H*N), the output projection and dZ take a grid column per
+    # feature group; 16384 is the widest model the library accepts.
     ("c4096-h4-n128-b1-t48", _w("c4096", 1, 48, 4096, 4, 128), None),
+    ("c5120-h40-n128-b1-t40", _w("c5120", 1, 40, 5120, 40, 128), None),
+    ("c8192-h8-n128-yarn4-b2-t24", _w("c8192", 2, 24, 8192, 8, 128, 4.0, 16), None),
+    ("c16384-h4-n128-b1-t20", _w("c16384", 1, 20, 16384, 4, 128), None),
     # C a multiple of 64 but not of 256 (any head count H at C = H*N): dx runs
     # the next wider layout with the features past C masked, the output
     # projection and dW end in partial 256-feature tiles.

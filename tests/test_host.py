@@ -137,10 +137,15 @@ def test_pointer_and_workspace_validation(lib):
         b_alias = list(bargs)
         b_alias[11] = bargs[other] + (4096 if other != 19 else 0)  # the workspace is 10 bytes here
         assert lib.mea_bwd(ctypes.byref(d), *b_alias, 10, None) == _header_enum("MEA_ERR_ALIAS")
-    # C above 4096 is refused in both passes.
-    d2 = _d(C=4352)
+    # C above 16384, or H*N*C of 2^29 or more (32-bit weight element
+    # indices), is refused in both passes.
+    d2 = _d(C=16416)
     assert lib.mea_bwd(ctypes.byref(d2), *bargs, 1 << 40, None) == _header_enum("MEA_ERR_MODEL_DIM")
+    d3 = _d(C=16384, H=256, N=128)
+    assert lib.mea_bwd(ctypes.byref(d3), *bargs, 1 << 40, None) == _header_enum("MEA_ERR_MODEL_DIM")
+    assert lib.mea_workspace_bytes(ctypes.byref(d3), _lib.MEA_PASS_FWD) == 0
     assert lib.mea_workspace_bytes(ctypes.byref(_d(C=2048, H=16, N=128)), _lib.MEA_PASS_BWD) > 0
+    assert lib.mea_workspace_bytes(ctypes.byref(_d(C=16384, H=8, N=128)), _lib.MEA_PASS_BWD) > 0
 
 
 def test_decode_and_prefill_validation(lib):
@@ -197,7 +202,7 @@ def test_varlen_validation(lib):
     # bwd: dy x wq wk wv wg wo f1 f2 o lse dx dwq dwk dwv dwg dwo df1 df2 ws
     bargs = [(1 << 32) + i * (1 << 28) for i in range(20)]
     assert lib.mea_bwd_varlen(ctypes.byref(d), fake, 4, 300, *bargs, 10, None) == _header_enum("MEA_ERR_WORKSPACE")
-    assert lib.mea_bwd_varlen(ctypes.byref(_d(B=1, T=1000, T_max=300, C=4352)), fake, 4, 300, *bargs, 1 << 40,
+    assert lib.mea_bwd_varlen(ctypes.byref(_d(B=1, T=1000, T_max=300, C=16416)), fake, 4, 300, *bargs, 1 << 40,
                               None) == _header_enum("MEA_ERR_MODEL_DIM")
 
 
