@@ -266,11 +266,15 @@ __device__ __forceinline__ int xcd_remap(int L, int G) {
 // tail_heads heads' worth of each XCD's range (at most a quarter of it, so
 // that long sequences keep their head-by-head L2 reuse) is taken
 // heaviest-first across those heads: the heaviest block of every one of its
-// heads first, then the next heaviest of each, and so on (modelled: 0.3% and
-// 1.1%). Any range of tail * nb consecutive items holds each block index
-// exactly tail times, so the tail is a permutation of itself whatever head
-// it starts in.
-constexpr int kTailHeads = 16;
+// heads first, then the next heaviest of each, and so on. Any range of
+// tail * nb consecutive items holds each block index exactly tail times, so
+// the tail is a permutation of itself whatever head it starts in. Four heads:
+// a wider tail balances the end better in a model, but its heads no longer
+// share L2 (B64 T4096 H8 N64 HBM reads per launch, forward / dQ / dK-dV:
+// 0 heads 0.83 / 2.29 / 2.26 GB, 4 heads 0.87 / 2.35 / 2.33 GB, 8 heads
+// 1.32 / 2.76 / 2.78 GB, 16 heads 2.66 / 4.01 / 4.10 GB) and 4 ran the
+// fastest step (8.25 ms against 8.29, 8.32 and 8.35 ms for 8, 16 and 0).
+constexpr int kTailHeads = 4;
 __device__ __forceinline__ int attn_item(int L, int G, int nb, int tail_heads = kTailHeads) {
   const int x = L & 7, i = L >> 3;
   const int q = G >> 3, rm = G & 7;
