@@ -30,8 +30,9 @@
  *   - Tensors are dense row-major in the shapes documented per argument.
  *     Pointers must be 16-byte aligned.
  *
- * Supported shapes: N in {64, 128, 256} (heads of 16 or 32 dimensions
- * zero-padded to N = 64, see N_active);
+ * Supported shapes: N in {32, 64, 128, 256}, with H even for N = 32 (the
+ * projection tiles hold head pairs); heads of 16 dimensions, and of 32 with
+ * H odd, are carried zero-padded to N = 32 or 64 (see N_active);
  * C a multiple of 32, 32 <= C <= 16384, with H * N * C < 2^29; H >= 1;
  * B, T >= 1; T <= T_max; and
  * for the backward H * (T + 256) * N < 2^30 (one batch's head-major gradient
@@ -56,7 +57,8 @@ typedef struct mea_desc {
   int64_t N;      /* head width */
   int64_t T_max;  /* rows of the rotary tables, >= T */
   float eps;      /* RMSNorm epsilon; the reference default is 1e-6 (fast_triton_attn.py:681) */
-  int64_t N_active; /* head dimensions in use: 0 (all N), or 16 or 32 with N = 64.
+  int64_t N_active; /* head dimensions in use: 0 (all N), 16 with N = 32, or 16
+                       or 32 with N = 64.
                        No counterpart in the reference: a head of N_active < N
                        dimensions is carried zero-padded to N (the last
                        N - N_active rows of every head in Wq, Wk, Wv, Wg and

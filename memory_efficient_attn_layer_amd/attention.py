@@ -32,8 +32,16 @@ import torch
 from . import _lib
 
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
-PADDED_HEAD_DIMS = (16, 32)  # carried zero-padded to PAD_N dimensions
-PAD_N = 64
+
+
+def storage_n(H: int, N: int) -> int:
+    """Head width the library runs for heads of N dimensions. The kernels
+    are built for 32, 64, 128 and 256; a 32-wide head needs an even H (the
+    projection tiles hold head pairs). Heads of 16 dimensions run zero-padded
+    to 32, and with an odd H heads of 16 or 32 run zero-padded to 64."""
+    if N >= 64:
+        return N
+    return 32 if H % 2 == 0 else 64
 MAX_C_FORWARD = 16384
 MAX_C_BACKWARD = 16384
 MAX_HN_C = 1 << 29  # H * N * C below this: 32-bit element indices into the stacked weights
@@ -84,21 +92,21 @@ def _validate(x, weights, factor1, factor2, H: int, N: int, eps: float, need_bac
         raise RuntimeError("fused_attn runs only on a ROCm GPU device (there is no CPU path)")
 
 
-def _pad_heads(H: int, N: int, weights, factor1, factor2):
-    """Zero-pads every head from N to PAD_N dimensions, differentiably (the
+def _pad_heads(H: int, N: int, weights, factor1, factor2, pad_n: int):
+    """Zero-pads every head from N to pad_n dimensions, differentiably (the
     gradients of the caller's tensors are the slices of the padded ones):
     rows of Wq, Wk, Wv, Wg and columns of Wo get zeros; the rotary tables get
     identity pairs (factor1 = 1, factor2 = 0), which keep the padded q and k
     dimensions at zero and the pair blocks invertible for the backward."""
     wq, wk, wv, wg, wo = weights
-    P = PAD_N - N
+    P = pad_n - N
 
     def rows(w):
         C = w.shape[1]
-        return torch.cat([w.reshape(H, N, C), w.new_zeros(H, P, C)], dim=1).reshape(H * PAD_N, C)
+        return torch.cat([w.reshape(H, N, C), w.new_zeros(H, P, C)], dim=1).reshape(H * pad_n, C)
 
     C = wo.shape[0]
-    wo_p = torch.cat([wo.reshape(C, H, N), wo.new_zeros(C, H, P)], dim=2).reshape(C, H * PAD_N)
+    wo_p = torch.cat([wo.reshape(C, H, N), wo.new_zeros(C, H, P)], dim=2).reshape(C, H * pad_n)
     f1_p = torch.cat([factor1, factor1.new_ones(factor1.shape[0], P)], dim=1)
     f2_p = torch.cat([factor2, factor2.new_zeros(factor2.shape[0], P)], dim=1)
     return (rows(wq), rows(wk), rows(wv), rows(wg), wo_p), f1_p, f2_p
@@ -135,10 +143,11 @@ class FusedAttentionFunction(torch.autograd.Function):
         save = _wants_grad(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2)
         weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
         H, N = int(H), int(N)
-        if N in PADDED_HEAD_DIMS:
+        Ns = storage_n(H, N) if N in SUPPORTED_HEAD_DIMS else N
+        if Ns != N:
             _validate(x, weights, factor1, factor2, H, N, float(eps), save)
-            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2)
-            return super().apply(x, *weights, factor1, factor2, H, PAD_N, eps, save, N)
+            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2, Ns)
+            return super().apply(x, *weights, factor1, factor2, H, Ns, eps, save, N)
         return super().apply(x, *weights, factor1, factor2, H, N, eps, save, 0)
 
     @staticmethod
@@ -244,12 +253,13 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         save = _wants_grad(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2)
         weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
         H, N = int(H), int(N)
-        if N in PADDED_HEAD_DIMS:
+        Ns = storage_n(H, N) if N in SUPPORTED_HEAD_DIMS else N
+        if Ns != N:
             if not isinstance(x, torch.Tensor) or x.dim() != 2:
                 raise ValueError("x must be a (total_tokens, C) tensor")
             _validate(x[:1].unsqueeze(0), weights, factor1, factor2, H, N, float(eps), save)
-            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2)
-            return super().apply(x, *weights, factor1, factor2, cu_seqlens, max_len, H, PAD_N, eps, save, N)
+            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2, Ns)
+            return super().apply(x, *weights, factor1, factor2, cu_seqlens, max_len, H, Ns, eps, save, N)
         return super().apply(x, *weights, factor1, factor2, cu_seqlens, max_len, H, N, eps, save, 0)
 
     @staticmethod

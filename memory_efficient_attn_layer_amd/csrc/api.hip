@@ -80,8 +80,11 @@ constexpr int64_t kMaxC = 16384;
 int validate(const mea_desc* d, int pass) {
   if (d == nullptr) return MEA_ERR_NULL;
   if (d->B < 1 || d->T < 1 || d->H < 1 || d->T_max < d->T) return MEA_ERR_SHAPE;
-  if (d->N != 64 && d->N != 128 && d->N != 256) return MEA_ERR_HEAD_DIM;
-  if (d->N_active != 0 && d->N_active != d->N && !(d->N == 64 && (d->N_active == 16 || d->N_active == 32)))
+  if (d->N != 32 && d->N != 64 && d->N != 128 && d->N != 256) return MEA_ERR_HEAD_DIM;
+  // 32-wide heads: the projection tiles hold head pairs.
+  if (d->N == 32 && d->H % 2 != 0) return MEA_ERR_HEAD_DIM;
+  if (d->N_active != 0 && d->N_active != d->N && !(d->N == 32 && d->N_active == 16) &&
+      !(d->N == 64 && (d->N_active == 16 || d->N_active == 32)))
     return MEA_ERR_HEAD_DIM;
   if (d->C < 32 || d->C % 32 != 0) return MEA_ERR_MODEL_DIM;
   const bool bwd = pass == MEA_PASS_BWD || pass == MEA_PASS_BWD_TABLES;

@@ -123,7 +123,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
         // Reduce the dot product over the CPR lanes of this row.
         dot += xor1(dot);
         dot += xor2(dot);
-        dot += shfl_xor(dot, 4);
+        if (CPR >= 8) dot += shfl_xor(dot, 4);
         if (CPR >= 16) dot += shfl_xor(dot, 8);
         if (CPR == 32) dot += shfl_xor(dot, 16);
         const float rr = rrw[k];
@@ -164,7 +164,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // (two blocks sharing every K/V fragment) held two per SIMD ran 4.4% slower.
 // ---------------------------------------------------------------------------
 template <int N, bool VARLEN>
-__global__ __launch_bounds__(256, N == 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   constexpr int QW = 32;                 // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
   constexpr int BQ = 4 * QW;             // queries per workgroup
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(256, N == 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
 // per SIMD.
 // ---------------------------------------------------------------------------
 template <int N, bool VARLEN>
-__global__ __launch_bounds__(256, N == 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_dkdv_kernel(AttnBwdParams p) {
   constexpr int KW = 32;                 // keys per wave
   constexpr int KB = KW / 32;            // 32-key MFMA blocks per wave
   static_assert(KB == 1, "one 32-key block per wave");
@@ -680,8 +680,11 @@ static hipError_t launch_bwd_variant(const AttnBwdParams& p, int N, int blocks_p
   // Grid: (sequence, head, block).
   const int G = (var ? p.nseq : p.B) * p.H * blocks_per_seq;
   if (G <= 0) return hipSuccess;
-  const int v = (N == 128 ? 2 : N == 256 ? 4 : 0) | (var ? 1 : 0);
+  if (N != 32 && N != 64 && N != 128 && N != 256) return hipErrorInvalidValue;
+  const int v = (N == 128 ? 2 : N == 256 ? 4 : N == 32 ? 6 : 0) | (var ? 1 : 0);
   switch (v) {
+    case 6: K<32, false>::launch(p, G, s); break;
+    case 7: K<32, true>::launch(p, G, s); break;
     case 0: K<64, false>::launch(p, G, s); break;
     case 1: K<64, true>::launch(p, G, s); break;
     case 2: K<128, false>::launch(p, G, s); break;
@@ -833,12 +836,16 @@ hipError_t launch_table_grad(const TableGradParams& p, int N, hipStream_t s) {
   constexpr int PT = 4;
   if (p.rows <= 0) return hipSuccess;
   const dim3 grid((p.rows + PT - 1) / PT);
-  if (N == 64)
+  if (N == 32)
+    hipLaunchKernelGGL(table_grad_kernel<32>, grid, dim3(256), 0, s, p);
+  else if (N == 64)
     hipLaunchKernelGGL(table_grad_kernel<64>, grid, dim3(256), 0, s, p);
   else if (N == 128)
     hipLaunchKernelGGL(table_grad_kernel<128>, grid, dim3(256), 0, s, p);
-  else
+  else if (N == 256)
     hipLaunchKernelGGL(table_grad_kernel<256>, grid, dim3(256), 0, s, p);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -47,7 +47,7 @@ namespace mea {
 // (sequence, h, query block) and every row index is taken relative to the
 // sequence's first token.
 template <int N, bool VARLEN>
-__global__ __launch_bounds__(256, N == 64 ? 4 : N == 128 ? 3 : 1) void attn_fwd_kernel(AttnFwdParams p) {
+__global__ __launch_bounds__(256, N <= 64 ? 4 : N == 128 ? 3 : 1) void attn_fwd_kernel(AttnFwdParams p) {
   constexpr int QW = 32;  // queries per wave
   constexpr int QB = QW / 32;            // 32-query MFMA blocks per wave
   constexpr int BQ = 4 * QW;             // queries per workgroup
@@ -193,13 +193,13 @@ __global__ __launch_bounds__(256, N == 64 ? 4 : N == 128 ? 3 : 1) void attn_fwd_
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       kf[ks] = as_frag(*reinterpret_cast<const u32x4*>(ks_t + st * 32 * N + koff[ks]));
-    // N = 64: the V^T fragments of the step are read with the K fragments,
-    // before the S products, and the scheduling fence keeps them there (128
-    // registers, still four workgroups per CU): read next to the PV products
-    // that use them, each read's LDS round trip stalled the wave (the kernel
-    // ran 1.9% slower). N = 128 and 256 have no registers to spare and read
-    // them at the products.
-    constexpr bool VEARLY = N == 64;
+    // N <= 64: the V^T fragments of the step are read with the K fragments,
+    // before the S products, and the scheduling fence keeps them there (N =
+    // 64: 128 registers, still four workgroups per CU): read next to the PV
+    // products that use them, each read's LDS round trip stalled the wave
+    // (the kernel ran 1.9% slower). N = 128 and 256 have no registers to
+    // spare and read them at the products.
+    constexpr bool VEARLY = N <= 64;
     auto vread = [&](int kst, int db) {
       const bf16_bits* vr = vs_t + (st * 32 + 16 * kst) * N;
       return frag_from2(lds_read_tr4(vr + voff[0][db]), lds_read_tr4(vr + voff[1][db]));
@@ -365,7 +365,11 @@ hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s) {
   const int BQ = 128;
   const bool var = p.cu != nullptr;
   const int G = var ? p.nseq * p.H * ((p.max_len + BQ - 1) / BQ) : p.B * p.H * ((p.T + BQ - 1) / BQ);
-  if (N == 64 && !var)
+  if (N == 32 && !var)
+    hipLaunchKernelGGL((attn_fwd_kernel<32, false>), dim3(G), dim3(256), 0, s, p);
+  else if (N == 32)
+    hipLaunchKernelGGL((attn_fwd_kernel<32, true>), dim3(G), dim3(256), 0, s, p);
+  else if (N == 64 && !var)
     hipLaunchKernelGGL((attn_fwd_kernel<64, false>), dim3(G), dim3(256), 0, s, p);
   else if (N == 64)
     hipLaunchKernelGGL((attn_fwd_kernel<64, true>), dim3(G), dim3(256), 0, s, p);
@@ -373,10 +377,12 @@ hipError_t launch_attn_fwd(const AttnFwdParams& p, int N, hipStream_t s) {
     hipLaunchKernelGGL((attn_fwd_kernel<128, false>), dim3(G), dim3(256), 0, s, p);
   else if (N == 128)
     hipLaunchKernelGGL((attn_fwd_kernel<128, true>), dim3(G), dim3(256), 0, s, p);
-  else if (!var)
+  else if (N == 256 && !var)
     hipLaunchKernelGGL((attn_fwd_kernel<256, false>), dim3(G), dim3(256), 0, s, p);
-  else
+  else if (N == 256)
     hipLaunchKernelGGL((attn_fwd_kernel<256, true>), dim3(G), dim3(256), 0, s, p);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -226,11 +226,16 @@ __device__ __forceinline__ u32x4 stat_sel_b(bool on) {
 //    bank line instead of stacking on one quarter of it.
 // p ^ ((p & 1) << 2) and r ^ ((r & 3) << 2) satisfy both. Rows of 32 chunks
 // (256 bf16) take the 16-chunk swizzle: it permutes the low four bits of the
-// slot, so 16 consecutive rows still fill 16 distinct bank groups.
+// slot, so 16 consecutive rows still fill 16 distinct bank groups. Rows of 4
+// chunks (32 bf16, 64 B): four rows share a bank line, so the four rows of
+// each residue r & 3 among 16 consecutive rows need distinct swizzles:
+// (r >> 2) & 3. A transposing read then covers 8 whole rows, two full bank
+// lines, whatever the swizzle.
 // Every swizzle depends on row & 15 only.
 template <int CH>
 __device__ __forceinline__ int chunk_swz(int row) {
-  static_assert(CH == 8 || CH == 16 || CH == 32, "rows of 64, 128 or 256 bf16");
+  static_assert(CH == 4 || CH == 8 || CH == 16 || CH == 32, "rows of 32, 64, 128 or 256 bf16");
+  if (CH == 4) return (row >> 2) & 3;
   if (CH == 8) {
     const int p = (row >> 1) & 7;
     return p ^ ((p & 1) << 2);

@@ -242,13 +242,14 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyParams p) {
   }
 }
 
-// Sum over the N threads of a workgroup (N = 64, 128 or 256: N / 64 waves,
-// added in wave order); every thread gets it.
+// Sum over the N threads of a workgroup (N = 32: the lower half of one
+// wave, whose exchanges stay inside it; 64, 128 or 256: N / 64 waves, added
+// in wave order); every thread gets it.
 template <int N>
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += shfl_xor(v, off);
-  if (N == 64) return v;
+  for (int off = (N < 64 ? N : 64) / 2; off > 0; off >>= 1) v += shfl_xor(v, off);
+  if (N <= 64) return v;
   __syncthreads();  // earlier readers of red are done
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -303,7 +304,9 @@ hipError_t launch_skinny_gemm(const SkinnyParams& p, hipStream_t s) {
 }
 
 hipError_t launch_decode_proj_epilogue(const DecodeProjParams& p, int N, hipStream_t s) {
-  if (N == 64)
+  if (N == 32)
+    hipLaunchKernelGGL(decode_proj_epilogue_kernel<32>, dim3(p.B * p.H), dim3(32), 0, s, p);
+  else if (N == 64)
     hipLaunchKernelGGL(decode_proj_epilogue_kernel<64>, dim3(p.B * p.H), dim3(64), 0, s, p);
   else if (N == 128)
     hipLaunchKernelGGL(decode_proj_epilogue_kernel<128>, dim3(p.B * p.H), dim3(128), 0, s, p);
@@ -330,7 +333,9 @@ void decode_splits(int B, int H, int Tc, int* S, int* chunk) {
 hipError_t launch_attn_decode(const DecodeParams& p, int N, hipStream_t s) {
   if (p.S % kDecodeWaves != 0 || p.chunk % 64 != 0) return hipErrorInvalidValue;
   const dim3 grid(p.B * p.H, p.S / kDecodeWaves);
-  if (N == 64)
+  if (N == 32)
+    hipLaunchKernelGGL(attn_decode_kernel<32>, grid, dim3(64 * kDecodeWaves), 0, s, p);
+  else if (N == 64)
     hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(64 * kDecodeWaves), 0, s, p);
   else if (N == 128)
     hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(64 * kDecodeWaves), 0, s, p);
@@ -342,7 +347,9 @@ hipError_t launch_attn_decode(const DecodeParams& p, int N, hipStream_t s) {
 }
 
 hipError_t launch_attn_decode_combine(const DecodeParams& p, int N, hipStream_t s) {
-  if (N == 64)
+  if (N == 32)
+    hipLaunchKernelGGL(attn_decode_combine_kernel<32>, dim3(p.B * p.H), dim3(256), 0, s, p);
+  else if (N == 64)
     hipLaunchKernelGGL(attn_decode_combine_kernel<64>, dim3(p.B * p.H), dim3(256), 0, s, p);
   else if (N == 128)
     hipLaunchKernelGGL(attn_decode_combine_kernel<128>, dim3(p.B * p.H), dim3(256), 0, s, p);

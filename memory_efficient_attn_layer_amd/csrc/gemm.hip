@@ -165,7 +165,7 @@ __global__ __launch_bounds__(TokShape<NF>::NT, 1) void dz_gate_bwd_kernel(DzPara
       }
       dl += xor1(dl);
       dl += xor2(dl);
-      dl += shfl_xor(dl, 4);
+      if (N >= 64) dl += shfl_xor(dl, 4);  // N is uniform
       if (N >= 128) dl += shfl_xor(dl, 8);
       if (N == 256) {
         // A 256-wide head spans waves wf and wf ^ 1 (heads align to the
@@ -197,7 +197,7 @@ static void launch_dz_nf(const DzParams& p, int HN, hipStream_t s) {
 
 hipError_t launch_dz_gate_bwd(const DzParams& p, hipStream_t s) {
   const int HN = p.H * p.N;
-  if (p.C % 32 != 0 || (p.N != 64 && p.N != 128 && p.N != 256)) return hipErrorInvalidValue;
+  if (p.C % 32 != 0 || (p.N != 32 && p.N != 64 && p.N != 128 && p.N != 256)) return hipErrorInvalidValue;
   // Feature groups of 512 where HN allows (see launch_gate_oproj).
   if (HN == 768)
     launch_dz_nf<768>(p, HN, s);

@@ -49,12 +49,21 @@ constexpr int kProjBF = 256;  // stacked-weight rows per tile
 constexpr int kProjBK = 32;   // k per slab
 constexpr int kProjStages = 3;
 
+// N = 32: a tile holds the four projections of a head pair, h is the pair
+// (heads 2h and 2h + 1; H is even).
 template <int N>
 __device__ __forceinline__ ProjTile proj_tile(int L, int H) {
-  constexpr int NFT = 4 * N / kProjBF;
-  const int tt = L / (H * NFT), rem = L - tt * (H * NFT);
-  return ProjTile{tt * kProjBT, rem / NFT, (rem % NFT) * kProjBF};
+  if constexpr (N == 32) {
+    const int np = H / 2, tt = L / np;
+    return ProjTile{tt * kProjBT, L - tt * np, 0};
+  } else {
+    constexpr int NFT = 4 * N / kProjBF;
+    const int tt = L / (H * NFT), rem = L - tt * (H * NFT);
+    return ProjTile{tt * kProjBT, rem / NFT, (rem % NFT) * kProjBF};
+  }
 }
+// Tiles of one 128-token tile: 4 * H * N stacked-weight rows in tiles of 256.
+__host__ __device__ __forceinline__ int proj_tiles_per_token_tile(int H, int N) { return H * 4 * N / kProjBF; }
 
 // Persistent: workgroups walk tiles; workgroup w runs on XCD w % 8 and takes
 // tiles from a contiguous range owned by that XCD, so the workgroups of one
@@ -96,7 +105,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   const int wf = wave % WF, wt = wave / WF;
 
   // This workgroup's tiles: start + j0 + i * nj for i < ntl.
-  const int ntiles = ((M + BT - 1) / BT) * H * (4 * N / BF);
+  const int ntiles = ((M + BT - 1) / BT) * proj_tiles_per_token_tile(H, N);
   const int G = gridDim.x, xcd = blockIdx.x & 7, j0 = blockIdx.x >> 3;
   const int nj = (G - xcd + 7) >> 3;
   const int q8 = ntiles >> 3, r8 = ntiles & 7;
@@ -127,6 +136,14 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
   auto plan_tile = [&](int ti) {
     const ProjTile tl = proj_tile<N>(start + j0 + ti * nj, H);
     iss_rot = tl.h % nk;
+    if constexpr (N == 32) {
+      // [q; v; k; g] of the head pair: rows 64h .. 64h + 63 of each matrix,
+      // one 64-row load group each, so each wave's 128 features hold the
+      // pair's rows of one rotary and one plain projection.
+      const bf16_bits* wsel[4] = {wq, wv, wk, wg};
+#pragma unroll
+      for (int u = 0; u < NUW; ++u) wbase[u] = wsel[u] + (size_t)(tl.h * 64) * w_row;
+    } else {
     const bf16_bits* wseg[NSEG];
     if (NSEG == 4) {
       // [q; v; k; g]: each wave's 128 features hold one rotary projection.
@@ -146,6 +163,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     for (int u = 0; u < NUW; ++u) {
       const int seg = (64 * u) / N;  // compile-time after unrolling
       wbase[u] = wseg[seg] + (size_t)(tl.h * N + 64 * u - seg * N) * w_row;
+    }
     }
 #pragma unroll
     for (int u = 0; u < NUX; ++u) xbase[u] = xg + (size_t)min(tl.m0 + 64 * u, M - 1) * C;
@@ -224,7 +242,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     const int m0 = tl.m0, h = tl.h;
     const int b0 = m0 / T, t0 = m0 - b0 * T;
     const bool tile_whole = m0 + BT <= M && t0 + BT <= T;
-    const bool has_rot = N == 64 || (N == 128 ? tl.f0 == 0 : tl.f0 < 2 * N);  // the wave holds q or k
+    const bool has_rot = N <= 64 || (N == 128 ? tl.f0 == 0 : tl.f0 < 2 * N);  // the wave holds q or k
     const int col = HALF ? wf * 128 : 0;  // first head column of the wave's features
     auto tab_row = [&](int tb) {
       const int m = m0 + wt * (TB * 16) + tb * 16 + c16;
@@ -321,9 +339,16 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
     // wave-uniform. For N = 64 the stacked rows are [q; v; k; g], so every
     // wave owns one rotary projection and one plain one and the epilogue work
     // is the same in all four waves; for N = 128 a tile is (q, k) or (v, g).
+    // N = 32: blocks 0, 1 are the rotary projection of heads 2h, 2h + 1 and
+    // blocks 2, 3 the plain one.
     auto proj_of = [&](int gi) {
-      return N == 64 ? (gi == 0 ? wf : 2 + wf) : N == 128 ? (tl.f0 == 0 ? 0 : 2) + wf : tl.f0 / N;
+      return N == 32   ? (gi < 2 ? wf : 2 + wf)
+             : N == 64 ? (gi == 0 ? wf : 2 + wf)
+             : N == 128 ? (tl.f0 == 0 ? 0 : 2) + wf
+                        : tl.f0 / N;
     };
+    // Head of the wave's gi-th N-feature block.
+    auto head_of = [&](int gi) { return N == 32 ? 2 * h + (gi & 1) : h; };
     constexpr int CPR = NW128 / 8;           // 16-byte chunks per staged row
     // Drains the staged block of projection gi for token block tb into
     // dstp + b * bstride + t * tstride.
@@ -379,7 +404,7 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       const float sc = rx[tb] * rr * (pj == 0 ? p.qscale : 1.0f);  // folded into the table rows
       if (ok[tb] && g == 0 && (!HALF || wf == 0)) {
         float* rstat = pj == 0 ? p.rq : p.rk;
-        if (rstat != nullptr) rstat[((size_t)brow[tb] * H + h) * T + t] = rr;
+        if (rstat != nullptr) rstat[((size_t)brow[tb] * H + head_of(gi)) * T + t] = rr;
       }
       float nrm = 0.f;
 #pragma unroll
@@ -428,13 +453,13 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
       }
     };
     auto drain_pj = [&](int gi, int tb) {
-      const int pj = proj_of(gi);
+      const int pj = proj_of(gi), hg = head_of(gi);
       if (pj < 2)
-        drain(gi, tb, (pj == 0 ? p.q : p.k) + (size_t)h * T * N + col, (size_t)H * T * N, (size_t)N);
+        drain(gi, tb, (pj == 0 ? p.q : p.k) + (size_t)hg * T * N + col, (size_t)H * T * N, (size_t)N);
       else if (pj == 2)
-        drain(gi, tb, p.v + (size_t)h * T * N + col, (size_t)H * T * N, (size_t)N);
+        drain(gi, tb, p.v + (size_t)hg * T * N + col, (size_t)H * T * N, (size_t)N);
       else
-        drain(gi, tb, p.sig + (size_t)h * N + col, (size_t)T * HN, (size_t)HN);
+        drain(gi, tb, p.sig + (size_t)hg * N + col, (size_t)T * HN, (size_t)HN);
     };
     if (N == 64) {
       // Plain (v or g) and rotary (q or k) blocks interleaved as P0 P1 R0 P2
@@ -453,6 +478,19 @@ __global__ __launch_bounds__(256, 2) void qkvg_proj_kernel(ProjParams p) {
         if (tb + 2 < TB) {
           plain_block(tb + 2, 1);
           drain_pj(1, tb + 2);
+        }
+      }
+    } else if (N == 32) {
+      // Per token block: the two heads' rotary blocks, then their plain ones.
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          if (gi < 2)
+            rot_block(tb, gi, -1);
+          else
+            plain_block(tb, gi);
+          drain_pj(gi, tb);
         }
       }
     } else {
@@ -516,13 +554,18 @@ static void launch_proj_n(const ProjParams& p, int G, hipStream_t s) {
 }
 
 hipError_t launch_qkvg_proj(const ProjParams& p, int N, hipStream_t s) {
-  const int G = persistent_grid(((p.M + kProjBT - 1) / kProjBT) * p.H * (4 * N / kProjBF), 2);
-  if (N == 64)
+  if (N == 32 && p.H % 2 != 0) return hipErrorInvalidValue;  // tiles hold head pairs
+  const int G = persistent_grid(((p.M + kProjBT - 1) / kProjBT) * proj_tiles_per_token_tile(p.H, N), 2);
+  if (N == 32)
+    launch_proj_n<32>(p, G, s);
+  else if (N == 64)
     launch_proj_n<64>(p, G, s);
   else if (N == 128)
     launch_proj_n<128>(p, G, s);
-  else
+  else if (N == 256)
     launch_proj_n<256>(p, G, s);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

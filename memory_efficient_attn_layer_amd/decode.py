@@ -21,26 +21,27 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .attention import MAX_C_FORWARD, PAD_N, PADDED_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _pad_heads, _validate
+from .attention import MAX_C_FORWARD, SUPPORTED_HEAD_DIMS, _pad_heads, _validate, storage_n
 
 
-def cache_width(N: int) -> int:
-    """Width of a cache row for heads of N dimensions: heads of 16 or 32
-    dimensions are carried zero-padded to PAD_N, as in fused_attn."""
-    return PAD_N if N in PADDED_HEAD_DIMS else N
+def cache_width(N: int, H: int) -> int:
+    """Width of a cache row for H heads of N dimensions: the head width the
+    library runs (storage_n; 16-wide heads zero-padded to 32, and to 64 with
+    an odd H, as in fused_attn)."""
+    return storage_n(H, N) if N in SUPPORTED_HEAD_DIMS else N
 
 
 @dataclass
 class KVCache:
-    """Per-layer cache: ``k`` and ``v`` of shape (B, H, capacity, cache_width(N)),
-    bf16 (heads of 16 or 32 dimensions as zero-padded rows of 64)."""
+    """Per-layer cache: ``k`` and ``v`` of shape (B, H, capacity, cache_width(N, H)),
+    bf16 (narrow heads as zero-padded rows, see cache_width)."""
 
     k: torch.Tensor
     v: torch.Tensor
 
     @classmethod
     def empty(cls, B: int, H: int, N: int, capacity: int, device) -> "KVCache":
-        shape = (B, H, capacity, cache_width(N))
+        shape = (B, H, capacity, cache_width(N, H))
         return cls(torch.zeros(shape, device=device, dtype=torch.bfloat16),
                    torch.zeros(shape, device=device, dtype=torch.bfloat16))
 
@@ -49,7 +50,7 @@ class KVCache:
         return self.k.shape[2]
 
     def check(self, B: int, H: int, N: int, device) -> None:
-        W = cache_width(N)
+        W = cache_width(N, H)
         for name, t in (("k", self.k), ("v", self.v)):
             if tuple(t.shape) != (B, H, self.capacity, W):
                 raise ValueError(f"cache.{name} has shape {tuple(t.shape)}, expected {(B, H, self.capacity, W)}")
@@ -60,13 +61,14 @@ class KVCache:
 
 
 def _padded(H: int, N: int, weights, factor1, factor2):
-    """(weights, tables, N, N_active) as the library takes them: heads of 16
-    or 32 dimensions zero-padded to PAD_N (no gradient is taken here)."""
-    if N not in PADDED_HEAD_DIMS:
+    """(weights, tables, N, N_active) as the library takes them: narrow heads
+    zero-padded to storage_n(H, N) (no gradient is taken here)."""
+    Ns = storage_n(H, N) if N in SUPPORTED_HEAD_DIMS else N
+    if Ns == N:
         return weights, factor1, factor2, N, 0
     with torch.no_grad():
-        w, f1, f2 = _pad_heads(H, N, weights, factor1, factor2)
-    return w, f1, f2, PAD_N, N
+        w, f1, f2 = _pad_heads(H, N, weights, factor1, factor2, Ns)
+    return w, f1, f2, Ns, N
 
 
 def _tables(factor1, factor2, rows: int):

@@ -177,27 +177,34 @@ def test_packed_bf16_tables_varlen_bitwise():
 
 @pytest.mark.parametrize("pad", ["identity", "zero"])
 @pytest.mark.parametrize("table_grad", [False, True], ids=["no-table-grad", "table-grad"])
-def test_narrow_heads_through_the_abi(pad, table_grad):
-    """Heads of 32 dimensions through the C ABI as the header describes them:
-    N = 64, N_active = 32, the last 32 rows of every head of Wq, Wk, Wv, Wg
-    and columns of Wo zero, and the padding columns of the rotary tables
-    holding identity pairs (f1 = 1, f2 = 0) or zeros. Both give the oracle's
-    N = 32 block (no NaN from the zero pair blocks in the backward)."""
+@pytest.mark.parametrize("n,ns", [(32, 64), (16, 32), (32, 32)], ids=["n32-in-64", "n16-in-32", "n32-native"])
+def test_narrow_heads_through_the_abi(n, ns, pad, table_grad):
+    """Narrow heads through the C ABI as the header describes them. Native:
+    N = 32 with an even H, no padding. Padded: N = ns, N_active = n, the
+    last ns - n rows of every head of Wq, Wk, Wv, Wg and columns of Wo zero,
+    and the padding columns of the rotary tables holding identity pairs
+    (f1 = 1, f2 = 0) or zeros. All give the oracle's N = n block (no NaN
+    from the zero pair blocks in the backward)."""
     from memory_efficient_attn_layer_amd.attention import _pad_heads
 
+    if ns == n and pad == "zero":
+        pytest.skip("no padding columns")
     lib = _lib.load()
-    w = Workload(99, "n32", 2, 150, 256, 4, 32, 4.0, 64)
+    w = Workload(99, f"n{n}", 2, 150, 256, 4, n, 4.0, 64)
     inp = make_inputs(w)
     ref = ob.block_grads(inp, w.H, w.N)
     g = {k: v.cuda().contiguous() for k, v in inp.items()}
-    wts, f1p, f2p = _pad_heads(w.H, w.N, [g[n] for n in ("wq", "wk", "wv", "wg", "wo")], g["f1"], g["f2"])
-    if pad == "zero":
-        f1p, f2p = f1p.clone(), f2p.clone()
-        f1p[:, w.N:] = 0
-    gp = dict(g, **{n: t.contiguous() for n, t in zip(("wq", "wk", "wv", "wg", "wo"), wts)})
-    wp = Workload(99, "n32p", w.B, w.T, w.C, w.H, 64)
+    if ns != n:
+        wts, f1p, f2p = _pad_heads(w.H, w.N, [g[m] for m in ("wq", "wk", "wv", "wg", "wo")], g["f1"], g["f2"], ns)
+        if pad == "zero":
+            f1p, f2p = f1p.clone(), f2p.clone()
+            f1p[:, w.N:] = 0
+        gp = dict(g, **{m: t.contiguous() for m, t in zip(("wq", "wk", "wv", "wg", "wo"), wts)})
+    else:
+        gp, f1p, f2p = g, g["f1"], g["f2"]
+    wp = Workload(99, f"n{n}p", w.B, w.T, w.C, w.H, ns)
     out = _run_block(lib, gp, f1p[:w.T].float().contiguous(), f2p[:w.T].float().contiguous(), wp, False,
-                     n_active=w.N, table_grad=table_grad)
+                     n_active=0 if ns == n else w.N, table_grad=table_grad)
     B, T, C, H, N = w.B, w.T, w.C, w.H, w.N
     for k, v in out.items():
         if v is not None:
@@ -205,10 +212,10 @@ def test_narrow_heads_through_the_abi(pad, table_grad):
     assert_out_close("y", out["y"].view(B, T, C), ref["y"])
     assert_grad_close("dx", out["dx"].view(B, T, C), ref["dx"])
     for k in ("dwq", "dwk", "dwv", "dwg"):
-        got = out[k].view(H, 64, C)
+        got = out[k].view(H, ns, C)
         assert torch.all(got[:, N:] == 0), f"{k}: padding rows nonzero"
         assert_grad_close(k, got[:, :N].reshape(H * N, C), ref[k])
-    assert_grad_close("dwo", out["dwo"].view(C, H, 64)[:, :, :N].reshape(C, H * N), ref["dwo"])
+    assert_grad_close("dwo", out["dwo"].view(C, H, ns)[:, :, :N].reshape(C, H * N), ref["dwo"])
     if table_grad:
-        assert_grad_close("df1", out["df1"].view(T, 64)[:, :N], ref["df1"][:T])
-        assert_grad_close("df2", out["df2"].view(T, 64)[:, :N], ref["df2"][:T])
+        assert_grad_close("df1", out["df1"].view(T, ns)[:, :N], ref["df1"][:T])
+        assert_grad_close("df2", out["df2"].view(T, ns)[:, :N], ref["df2"][:T])

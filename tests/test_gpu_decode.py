@@ -51,8 +51,8 @@ class _Block:
 
 @pytest.mark.parametrize(
     "C,H,N",
-    [(256, 2, 64), (512, 4, 128), (512, 2, 256), (96, 3, 32), (64, 4, 16)],
-    ids=["c256-h2-n64", "c512-h4-n128", "c512-h2-n256", "c96-h3-n32-padded", "c64-h4-n16-padded"],
+    [(256, 2, 64), (512, 4, 128), (512, 2, 256), (96, 3, 32), (64, 4, 16), (256, 8, 32)],
+    ids=["c256-h2-n64", "c512-h4-n128", "c512-h2-n256", "c96-h3-n32-padded", "c64-h4-n16-padded", "c256-h8-n32"],
 )
 def test_prefill_then_decode_matches_oracle(C, H, N):
     B, T0, steps, cap = 2, 37, 3, 64
@@ -162,7 +162,7 @@ def test_prefill_with_bf16_tables_is_bitwise_the_fp32_copy(C, H, N):
     assert_out_close("y", outs[0][0], ref)
 
 
-@pytest.mark.parametrize("C,H,N", [(512, 4, 128), (128, 4, 32)], ids=["n128", "n32-padded"])
+@pytest.mark.parametrize("C,H,N", [(512, 4, 128), (128, 4, 32), (96, 3, 32)], ids=["n128", "n32", "n32-padded"])
 def test_decode_graph_replays_match_eager_steps(C, H, N):
     # Captured decode steps, replayed several times with eager work and
     # synchronisation between the replays; every replay must equal the eager

@@ -29,6 +29,7 @@ STAGE_CASES = [
     ("cfg3-b1-t512", _w("c3", 1, 512, 1024, 8, 128), None),
     ("ragged-b3-t77", _w("r", 3, 77, 256, 2, 64), None),
     ("yarn4-b1-t300", _w("y", 1, 300, 512, 4, 64, 4.0, 128), None),
+    ("n32-yarn4-b2-t300", _w("n32", 2, 300, 256, 8, 32, 4.0, 128), None),
     # Forward-only widths (C > 1024): the output projection in 256- and
     # 512-feature groups.
     ("c1280-h4-b1-t64", _w("c1280", 1, 64, 1280, 4, 64), None),
@@ -129,16 +130,22 @@ BLOCK_CASES = [
     # own buffer (H*N > C); 300 tokens end in a partial block.
     ("c800-hn512-b2-t150", _w("c800", 2, 150, 800, 8, 64), None),
     ("c928-hn1024-n128-b1-t300", _w("c928", 1, 300, 928, 8, 128), None),
-    # Heads of 32 and 16 dimensions (carried zero-padded to 64; the head
-    # RMSNorm and the attention scale use the true width).
+    # Heads of 32 dimensions with an even H run natively (projection tiles of
+    # head pairs, 32-wide attention tiles); heads of 16 run zero-padded to
+    # 32 (the head RMSNorm and the attention scale use the true width).
     ("n32-h8-c256-b2-t100", _w("n32", 2, 100, 256, 8, 32), None),
     ("n32-yarn4-h6-c192-b1-t300", _w("n32y", 1, 300, 192, 6, 32, 4.0, 128), None),
+    ("n32-h16-c512-b1-t700", _w("n32l", 1, 700, 512, 16, 32), None),
+    ("n32-h2-c640-b2-t129", _w("n32c", 2, 129, 640, 2, 32), None),
     ("n16-h4-c64-b2-t70", _w("n16", 2, 70, 64, 4, 16), None),
-    # C = H*N a multiple of 32 only (odd H with N = 32, H = 2 with N = 16; a
-    # wide C whose last dx feature group holds 32 features).
+    ("n16-yarn4-h8-c128-b1-t333", _w("n16y", 1, 333, 128, 8, 16, 4.0, 64), None),
+    # C = H*N a multiple of 32 only (odd H with N = 32 or 16: zero-padded to
+    # 64; H = 2 with N = 16; a wide C whose last dx feature group holds 32
+    # features).
     ("n32-h3-c96-b2-t90", _w("n32h3", 2, 90, 96, 3, 32), None),
     ("n16-h2-c32-b2-t64", _w("n16h2", 2, 64, 32, 2, 16), None),
     ("n32-h33-c1056-b1-t50", _w("n32w", 1, 50, 1056, 33, 32), None),
+    ("n16-h5-c96-b1-t60", _w("n16h5", 1, 60, 96, 5, 16), None),
     # Heads of 256 dimensions: one wave per SIMD in the attention kernels,
     # 32-query tiles in dK/dV, the projection's and dZ's head sums over two
     # waves.

@@ -72,9 +72,11 @@ def _oracle(inp, lens, H, N):
 @pytest.mark.parametrize(
     "lens,C,H,N",
     [([77, 256, 300, 1, 513], 256, 2, 64), ([130, 64, 200], 512, 4, 128), ([90, 33, 160], 512, 2, 256),
-     ([70, 130], 96, 3, 32), ([0, 90, 0, 0, 45], 256, 2, 64), ([100, 57, 130], 1024, 8, 64)],
+     ([70, 130], 96, 3, 32), ([0, 90, 0, 0, 45], 256, 2, 64), ([100, 57, 130], 1024, 8, 64),
+     ([70, 0, 200, 33], 128, 4, 32), ([50, 129], 64, 4, 16)],
     # c1024: dx in two 512-feature groups over the packed tokens (a partial last block).
-    ids=["n64-5seq", "n128-3seq", "n256-3seq", "n32-2seq", "n64-empty-seqs", "c1024-3seq"],
+    ids=["n64-5seq", "n128-3seq", "n256-3seq", "n32-padded-2seq", "n64-empty-seqs", "c1024-3seq", "n32-4seq",
+         "n16-2seq"],
 )
 def test_varlen_forward_backward_matches_oracle_per_sequence(lens, C, H, N):
     inp = _inputs(lens, C, H, N, t_max=max(lens) + 40, seed=21)

@@ -87,7 +87,9 @@ def test_workspace_bytes(lib):
 @pytest.mark.parametrize(
     "kw,code",
     [
-        (dict(N=32), "MEA_ERR_HEAD_DIM"),
+        (dict(N=32, H=3), "MEA_ERR_HEAD_DIM"),
+        (dict(N=16), "MEA_ERR_HEAD_DIM"),
+        (dict(N=32, N_active=8), "MEA_ERR_HEAD_DIM"),
         (dict(N=512), "MEA_ERR_HEAD_DIM"),
         (dict(N_active=48), "MEA_ERR_HEAD_DIM"),
         (dict(N=128, N_active=32), "MEA_ERR_HEAD_DIM"),
@@ -301,11 +303,24 @@ def test_static_decode_validation(lib):
     assert int(m.group(1)) << int(m.group(2)) == _lib.MEA_STATIC_SCRATCH_BYTES
 
 
-def test_descriptor_accepts_padded_heads(lib):
-    """Heads of 16 or 32 dimensions are described as N = 64 with N_active."""
+def test_descriptor_accepts_narrow_heads(lib):
+    """32-wide heads run natively with an even H; heads of 16 dimensions are
+    described as N = 32 (or 64) with N_active, 32 with an odd H as N = 64."""
     for n_act in (0, 16, 32, 64):
         assert lib.mea_workspace_bytes(ctypes.byref(_d(N_active=n_act)), _lib.MEA_PASS_FWD) > 0
+    for n_act in (0, 16, 32):
+        assert lib.mea_workspace_bytes(ctypes.byref(_d(N=32, N_active=n_act)), _lib.MEA_PASS_BWD) > 0
     assert lib.mea_workspace_bytes(ctypes.byref(_d(N=128, N_active=128)), _lib.MEA_PASS_BWD) > 0
+
+
+def test_storage_width_of_narrow_heads():
+    """storage_n: the head width the library runs for each (H, N)."""
+    from memory_efficient_attn_layer_amd.attention import storage_n
+    from memory_efficient_attn_layer_amd.decode import cache_width
+
+    assert [storage_n(4, n) for n in (16, 32, 64, 128, 256)] == [32, 32, 64, 128, 256]
+    assert [storage_n(3, n) for n in (16, 32, 64, 128, 256)] == [64, 64, 64, 128, 256]
+    assert cache_width(32, 8) == 32 and cache_width(16, 8) == 32 and cache_width(32, 5) == 64
 
 
 def test_pad_heads_layout_and_gradients():
@@ -313,14 +328,15 @@ def test_pad_heads_layout_and_gradients():
     (columns of Wo, table columns) in place, the padding is zero (identity
     rotary pairs in the tables), and gradients of the padded tensors reach
     the caller's tensors as their slices."""
-    from memory_efficient_attn_layer_amd.attention import PAD_N, _pad_heads
+    from memory_efficient_attn_layer_amd.attention import _pad_heads
 
+    PAD_N = 64
     torch.manual_seed(0)
     H, N, C, T = 3, 32, 96, 10
     ws = [torch.randn(H * N, C, requires_grad=True) for _ in range(4)] + [torch.randn(C, H * N, requires_grad=True)]
     f1 = torch.randn(T, N, requires_grad=True)
     f2 = torch.randn(T, N, requires_grad=True)
-    (wq, wk, wv, wg, wo), p1, p2 = _pad_heads(H, N, ws, f1, f2)
+    (wq, wk, wv, wg, wo), p1, p2 = _pad_heads(H, N, ws, f1, f2, PAD_N)
     assert wq.shape == (H * PAD_N, C) and wo.shape == (C, H * PAD_N) and p1.shape == (T, PAD_N)
     for h in range(H):
         assert torch.equal(wq[h * PAD_N:h * PAD_N + N], ws[0][h * N:(h + 1) * N])
