@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
   if constexpr (!VARLEN) {
     T = p.T;
     const int nqb = (T + BQ - 1) / BQ;
-    const int lid = attn_item(blockIdx.x, p.B * nh * nqb, nqb);
+    const int lid = attn_item(blockIdx.x, p.B * nh * nqb, nqb, N <= 64 ? 3 : 1);
     const int bh = lid / nqb;
     qi = nqb - 1 - lid % nqb;
     b = bh / nh;
@@ -449,7 +449,7 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
   if constexpr (!VARLEN) {
     T = p.T;
     const int nkb = (T + BKV - 1) / BKV;
-    const int lid = attn_item(blockIdx.x, p.B * nh * nkb, nkb);
+    const int lid = attn_item(blockIdx.x, p.B * nh * nkb, nkb, N <= 64 ? 3 : 1);
     const int bh = lid / nkb;
     ki = lid % nkb;
     b = bh / nh;

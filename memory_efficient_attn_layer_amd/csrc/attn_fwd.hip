@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256, N <= 64 ? 4 : N == 128 ? 3 : 1) void attn_fwd_
   if constexpr (!VARLEN) {
     T = p.T;
     const int nqb = (T + BQ - 1) / BQ;
-    const int lid = attn_item(blockIdx.x, p.B * p.H * nqb, nqb);
+    const int lid = attn_item(blockIdx.x, p.B * p.H * nqb, nqb, N <= 64 ? 3 : 1);
     bh = lid / nqb;
     qi = nqb - 1 - lid % nqb;
     b = bh / p.H;

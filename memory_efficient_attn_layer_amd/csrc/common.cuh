@@ -253,7 +253,7 @@ __device__ __forceinline__ int swz_off(int row, int col) {
 // The hardware hands workgroup L to XCD L % 8; logical tile ids
 // [start(x), start(x)+count(x)) are made to run on XCD x, which keeps
 // neighbouring tiles (that share operand rows) inside one L2.
-__device__ __forceinline__ int xcd_remap(int L, int G) {
+__host__ __device__ __forceinline__ int xcd_remap(int L, int G) {
   const int x = L & 7, i = L >> 3;
   const int q = G >> 3, r = G & 7;
   const int start = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
@@ -280,14 +280,39 @@ __device__ __forceinline__ int xcd_remap(int L, int G) {
 // 1.32 / 2.76 / 2.78 GB, 16 heads 2.66 / 4.01 / 4.10 GB) and 4 ran the
 // fastest step (8.25 ms against 8.29, 8.32 and 8.35 ms for 8, 16 and 0).
 constexpr int kTailHeads = 4;
-__device__ __forceinline__ int attn_item(int L, int G, int nb, int tail_heads = kTailHeads) {
+// Before the tail, the order is dealt out so that the workgroups sharing a
+// CU run blocks of different weight. In plain order, an XCD's first
+// kCusPerXcd * slots workgroups (which fill its CUs, slots = workgroups per
+// CU) would put the same block index of consecutive heads on the slots of a
+// CU: blocks of the same length, which start, wait for their first tiles,
+// run their epilogues and finish in step, leaving the matrix cores to fewer
+// waves each time. So within every run of kCusPerXcd * slots items, the
+// items of slot j = r / kCusPerXcd (r the position in the run) are rotated
+// by j * ceil(kCusPerXcd / slots): a permutation of the run, whose slots
+// start blocks a third of a head apart. Measured on B64 T4096 H8 N64 (same
+// box, rotation against plain order, three runs on three boxes): dK/dV
+// -2.3 to -3.4%, dQ -1.4 to -2.6%, forward -0.9 to -1.5% (three slots in
+// all three kernels; four in the forward, its occupancy, gained 0.2%); the
+// step -0.5 to -1.3%. With 128-wide heads (two slots) dK/dV ran 1.1% slower
+// and T = 32768 was unchanged, so only N <= 64 uses it (slots = 1: plain).
+constexpr int kCusPerXcd = 32;
+// (Host and device: tests/work_order.cpp checks on the CPU that it is a
+// permutation of 0 .. G - 1.)
+__host__ __device__ __forceinline__ int attn_item(int L, int G, int nb, int slots, int tail_heads = kTailHeads) {
   const int x = L & 7, i = L >> 3;
   const int q = G >> 3, rm = G & 7;
   const int n = q + (x < rm ? 1 : 0);
   const int s = x < rm ? x * (q + 1) : rm * (q + 1) + (x - rm) * q;
-  const int th = n < nb ? 0 : min(tail_heads, max(1, n / nb / 4));  // heads in the tail (th * nb <= n)
+  const int h4 = n / nb / 4 > 1 ? n / nb / 4 : 1;
+  const int th = n < nb ? 0 : (tail_heads < h4 ? tail_heads : h4);  // heads in the tail (th * nb <= n)
   const int R = th * nb;
-  if (i < n - R) return s + i;
+  if (i < n - R) {
+    const int run = kCusPerXcd * slots, blk = i / run, r = i - blk * run;
+    if (slots == 1 || (blk + 1) * run > n - R) return s + i;  // the last partial run: as is
+    const int slot = r / kCusPerXcd, c = r - slot * kCusPerXcd;
+    const int rot = slot * ((kCusPerXcd + slots - 1) / slots);
+    return s + blk * run + slot * kCusPerXcd + (c + rot) % kCusPerXcd;
+  }
   const int j = i - (n - R);
   const int k = j / th, c = j - k * th;     // block k (heaviness rank), its c-th head in the tail
   const int base = s + n - R;

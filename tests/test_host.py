@@ -395,3 +395,24 @@ def test_varlen_host_offsets_are_checked():
     with pytest.raises(ValueError, match="nseq"):
         fused_attn_varlen(*args, [300])
     assert check_offsets([0, 100, 100, 300], 300) == 200  # empty sequences are fine
+
+
+def test_attention_work_order_is_a_permutation(tmp_path):
+    """The attention kernels' workgroup -> (b, h, block) order (attn_item in
+    csrc/common.cuh: per-XCD ranges, the slot rotation, the heaviest-first
+    tail) is a permutation for every grid size, blocks per head and slot
+    count: compiled for the host from the kernels' own header and
+    enumerated on the CPU (tests/work_order.cpp)."""
+    import shutil
+    import subprocess
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not found")
+    exe = tmp_path / "work_order"
+    src = Path(__file__).resolve().parent / "work_order.cpp"
+    subprocess.run([hipcc, "--cuda-host-only", "-x", "hip", "-O2", "-std=c++17", str(src), "-o", str(exe)],
+                   check=True, capture_output=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert res.stdout.startswith("ok ")
