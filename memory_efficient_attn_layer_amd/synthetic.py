@@ -49,6 +49,9 @@ WORKLOADS = {
     2: Workload(2, "long-context-yarn4 B8 T32768 C512 H8 N64", 8, 32768, 512, 8, 64, 4.0, 8192),
     3: Workload(3, "wide-head B16 T8192 C1024 H8 N128", 16, 8192, 1024, 8, 128),
     4: Workload(4, "prefill-yarn8 B1 T131072 C2048 H16 N128", 1, 131072, 2048, 16, 128, 8.0, 16384, False),
+    # Not one of the five configurations: the pretrain width with 32-wide
+    # heads (the native N = 32 kernels), for the benchmark only.
+    5: Workload(5, "narrow-head B32 T4096 C512 H16 N32", 32, 4096, 512, 16, 32),
 }
 
 
