@@ -934,7 +934,7 @@ const char* mea_strerror(int code) {
     case MEA_OK: return "ok";
     case MEA_ERR_NULL: return "a required pointer is NULL (or only one of a pair was given)";
     case MEA_ERR_SHAPE: return "B, T, H must be >= 1, T <= T_max, and indices must fit 31 bits";
-    case MEA_ERR_HEAD_DIM: return "head width N must be 64, 128 or 256";
+    case MEA_ERR_HEAD_DIM: return "head width N must be 32 (with H even), 64, 128 or 256, N_active 0, N or 16 (N = 32, 64) or 32 (N = 64)";
     case MEA_ERR_MODEL_DIM: return "model width C must be a multiple of 32 in [32, 16384] with H*N*C < 2^29";
     case MEA_ERR_WORKSPACE: return "workspace smaller than mea_workspace_bytes()";
     case MEA_ERR_ALIGN: return "a pointer is not 16-byte aligned";
