@@ -31,8 +31,10 @@
  *     Pointers must be 16-byte aligned.
  *
  * Supported shapes: N in {32, 64, 128, 256}, with H even for N = 32 (the
- * projection tiles hold head pairs); heads of 16 dimensions, and of 32 with
- * H odd, are carried zero-padded to N = 32 or 64 (see N_active);
+ * projection tiles hold head pairs); heads of 16 dimensions are carried
+ * zero-padded to N = 32 or 64 (see N_active), and an odd number of 16- or
+ * 32-wide heads with one zero head more (zero weight rows and Wo columns)
+ * or as N = 64;
  * C a multiple of 32, 32 <= C <= 16384, with H * N * C < 2^29; H >= 1;
  * B, T >= 1; T <= T_max; and
  * for the backward H * (T + 256) * N < 2^30 (one batch's head-major gradient

@@ -20,10 +20,11 @@ Differences from the reference, all deliberate:
   * Rotary tables may be bf16, fp16 or fp32 (the reference accepts only bf16).
   * Without a gradient requirement the forward keeps no activations.
   * Unsupported shapes raise ValueError before any launch.
-  * Heads of 16 or 32 dimensions run zero-padded to 64 (zero weight rows
-    and o_proj columns, identity rotary pairs); the head RMSNorm and the
-    attention scale use the true head width, so results are those of the
-    unpadded block, at the cost of the padded width.
+  * Heads of 32 dimensions run natively; heads of 16 run zero-padded to 32
+    (zero weight rows and o_proj columns, identity rotary pairs), and an
+    odd number of 16- or 32-wide heads gets one zero head more (the kernels
+    take 32-wide heads in pairs); the head RMSNorm and the attention scale
+    use the true head width, so results are those of the unpadded block.
 """
 from __future__ import annotations
 
@@ -34,14 +35,20 @@ from . import _lib
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 
+def storage_shape(H: int, N: int) -> tuple[int, int]:
+    """(heads, head width) the library runs for H heads of N dimensions. The
+    kernels are built for widths 32, 64, 128 and 256, and 32-wide heads come
+    in pairs (the projection tiles hold head pairs): heads of 16 dimensions
+    run zero-padded to 32, and an odd number of 16- or 32-wide heads gets one
+    zero head more."""
+    if N >= 64 or N not in SUPPORTED_HEAD_DIMS:
+        return H, N
+    return H + (H & 1), 32
+
+
 def storage_n(H: int, N: int) -> int:
-    """Head width the library runs for heads of N dimensions. The kernels
-    are built for 32, 64, 128 and 256; a 32-wide head needs an even H (the
-    projection tiles hold head pairs). Heads of 16 dimensions run zero-padded
-    to 32, and with an odd H heads of 16 or 32 run zero-padded to 64."""
-    if N >= 64:
-        return N
-    return 32 if H % 2 == 0 else 64
+    """Head width the library runs (storage_shape)."""
+    return storage_shape(H, N)[1]
 MAX_C_FORWARD = 16384
 MAX_C_BACKWARD = 16384
 MAX_HN_C = 1 << 29  # H * N * C below this: 32-bit element indices into the stacked weights
@@ -92,21 +99,27 @@ def _validate(x, weights, factor1, factor2, H: int, N: int, eps: float, need_bac
         raise RuntimeError("fused_attn runs only on a ROCm GPU device (there is no CPU path)")
 
 
-def _pad_heads(H: int, N: int, weights, factor1, factor2, pad_n: int):
-    """Zero-pads every head from N to pad_n dimensions, differentiably (the
-    gradients of the caller's tensors are the slices of the padded ones):
-    rows of Wq, Wk, Wv, Wg and columns of Wo get zeros; the rotary tables get
-    identity pairs (factor1 = 1, factor2 = 0), which keep the padded q and k
-    dimensions at zero and the pair blocks invertible for the backward."""
+def _pad_heads(H: int, N: int, weights, factor1, factor2, pad_n: int, pad_h: int | None = None):
+    """Zero-pads every head from N to pad_n dimensions and the head count
+    from H to pad_h (zero heads), differentiably (the gradients of the
+    caller's tensors are the slices of the padded ones): rows of Wq, Wk, Wv,
+    Wg and columns of Wo get zeros; the rotary tables get identity pairs
+    (factor1 = 1, factor2 = 0), which keep the padded q and k dimensions at
+    zero and the pair blocks invertible for the backward. A zero head has
+    q = k = v = 0 and a zero column block in Wo: it adds nothing to y, and
+    every gradient it produces is zero (dZ = dy Wo is zero on it)."""
     wq, wk, wv, wg, wo = weights
-    P = pad_n - N
+    pad_h = H if pad_h is None else pad_h
+    P, Q = pad_n - N, pad_h - H
 
     def rows(w):
         C = w.shape[1]
-        return torch.cat([w.reshape(H, N, C), w.new_zeros(H, P, C)], dim=1).reshape(H * pad_n, C)
+        w3 = torch.cat([w.reshape(H, N, C), w.new_zeros(H, P, C)], dim=1)
+        return torch.cat([w3, w.new_zeros(Q, pad_n, C)], dim=0).reshape(pad_h * pad_n, C)
 
     C = wo.shape[0]
-    wo_p = torch.cat([wo.reshape(C, H, N), wo.new_zeros(C, H, P)], dim=2).reshape(C, H * pad_n)
+    wo3 = torch.cat([wo.reshape(C, H, N), wo.new_zeros(C, H, P)], dim=2)
+    wo_p = torch.cat([wo3, wo.new_zeros(C, Q, pad_n)], dim=1).reshape(C, pad_h * pad_n)
     f1_p = torch.cat([factor1, factor1.new_ones(factor1.shape[0], P)], dim=1)
     f2_p = torch.cat([factor2, factor2.new_zeros(factor2.shape[0], P)], dim=1)
     return (rows(wq), rows(wk), rows(wv), rows(wg), wo_p), f1_p, f2_p
@@ -143,11 +156,11 @@ class FusedAttentionFunction(torch.autograd.Function):
         save = _wants_grad(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2)
         weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
         H, N = int(H), int(N)
-        Ns = storage_n(H, N) if N in SUPPORTED_HEAD_DIMS else N
-        if Ns != N:
+        Hs, Ns = storage_shape(H, N)
+        if (Hs, Ns) != (H, N):
             _validate(x, weights, factor1, factor2, H, N, float(eps), save)
-            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2, Ns)
-            return super().apply(x, *weights, factor1, factor2, H, Ns, eps, save, N)
+            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2, Ns, Hs)
+            return super().apply(x, *weights, factor1, factor2, Hs, Ns, eps, save, N if Ns != N else 0)
         return super().apply(x, *weights, factor1, factor2, H, N, eps, save, 0)
 
     @staticmethod
@@ -253,13 +266,14 @@ class FusedAttentionVarlenFunction(torch.autograd.Function):
         save = _wants_grad(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor2)
         weights = (q_weight, k_weight, v_weight, g_weight, o_weight)
         H, N = int(H), int(N)
-        Ns = storage_n(H, N) if N in SUPPORTED_HEAD_DIMS else N
-        if Ns != N:
+        Hs, Ns = storage_shape(H, N)
+        if (Hs, Ns) != (H, N):
             if not isinstance(x, torch.Tensor) or x.dim() != 2:
                 raise ValueError("x must be a (total_tokens, C) tensor")
             _validate(x[:1].unsqueeze(0), weights, factor1, factor2, H, N, float(eps), save)
-            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2, Ns)
-            return super().apply(x, *weights, factor1, factor2, cu_seqlens, max_len, H, Ns, eps, save, N)
+            weights, factor1, factor2 = _pad_heads(H, N, weights, factor1, factor2, Ns, Hs)
+            return super().apply(x, *weights, factor1, factor2, cu_seqlens, max_len, Hs, Ns, eps, save,
+                                 N if Ns != N else 0)
         return super().apply(x, *weights, factor1, factor2, cu_seqlens, max_len, H, N, eps, save, 0)
 
     @staticmethod

@@ -5,8 +5,9 @@ The reference trains only and has no decode path; these run the same block
 math (README.md:42-64) through ``mea_prefill`` / ``mea_decode`` of libmea.so.
 The cache holds, per (batch, head), the k rows exactly as the attention uses
 them (RMS-normalised over N and rotated) and the plain v rows, bf16, in a
-``(B, H, capacity, cache_width(N))`` layout (heads of 16 or 32 dimensions are
-held zero-padded to 64). Sequence b's new token sits at position
+``(B, cache_heads(N, H), capacity, cache_width(N, H))`` layout (heads of 16
+dimensions are held zero-padded to 32, and an odd number of 16- or 32-wide
+heads with one zero head more). Sequence b's new token sits at position
 ``pos[b]``: it reads rotary row ``pos[b]``, its k / v are written to cache row
 ``pos[b]``, and it attends to rows ``0 .. pos[b]``, so sequences of a batch may
 have different lengths.
@@ -21,27 +22,34 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .attention import MAX_C_FORWARD, SUPPORTED_HEAD_DIMS, _pad_heads, _validate, storage_n
+from .attention import MAX_C_FORWARD, SUPPORTED_HEAD_DIMS, _pad_heads, _validate, storage_shape
 
 
 def cache_width(N: int, H: int) -> int:
     """Width of a cache row for H heads of N dimensions: the head width the
-    library runs (storage_n; 16-wide heads zero-padded to 32, and to 64 with
-    an odd H, as in fused_attn)."""
-    return storage_n(H, N) if N in SUPPORTED_HEAD_DIMS else N
+    library runs (storage_shape; 16-wide heads zero-padded to 32, as in
+    fused_attn)."""
+    return storage_shape(H, N)[1]
+
+
+def cache_heads(N: int, H: int) -> int:
+    """Heads of a cache for H heads of N dimensions (storage_shape: an odd
+    number of 16- or 32-wide heads carries one zero head more)."""
+    return storage_shape(H, N)[0]
 
 
 @dataclass
 class KVCache:
-    """Per-layer cache: ``k`` and ``v`` of shape (B, H, capacity, cache_width(N, H)),
-    bf16 (narrow heads as zero-padded rows, see cache_width)."""
+    """Per-layer cache: ``k`` and ``v`` of shape (B, cache_heads(N, H), capacity,
+    cache_width(N, H)), bf16 (narrow heads as zero-padded rows, an odd number
+    of them with one zero head more; see storage_shape)."""
 
     k: torch.Tensor
     v: torch.Tensor
 
     @classmethod
     def empty(cls, B: int, H: int, N: int, capacity: int, device) -> "KVCache":
-        shape = (B, H, capacity, cache_width(N, H))
+        shape = (B, cache_heads(N, H), capacity, cache_width(N, H))
         return cls(torch.zeros(shape, device=device, dtype=torch.bfloat16),
                    torch.zeros(shape, device=device, dtype=torch.bfloat16))
 
@@ -50,10 +58,10 @@ class KVCache:
         return self.k.shape[2]
 
     def check(self, B: int, H: int, N: int, device) -> None:
-        W = cache_width(N, H)
+        W, Hc = cache_width(N, H), cache_heads(N, H)
         for name, t in (("k", self.k), ("v", self.v)):
-            if tuple(t.shape) != (B, H, self.capacity, W):
-                raise ValueError(f"cache.{name} has shape {tuple(t.shape)}, expected {(B, H, self.capacity, W)}")
+            if tuple(t.shape) != (B, Hc, self.capacity, W):
+                raise ValueError(f"cache.{name} has shape {tuple(t.shape)}, expected {(B, Hc, self.capacity, W)}")
             if t.dtype != torch.bfloat16 or not t.is_contiguous():
                 raise ValueError(f"cache.{name} must be a contiguous bfloat16 tensor")
             if t.device != device:
@@ -61,14 +69,14 @@ class KVCache:
 
 
 def _padded(H: int, N: int, weights, factor1, factor2):
-    """(weights, tables, N, N_active) as the library takes them: narrow heads
-    zero-padded to storage_n(H, N) (no gradient is taken here)."""
-    Ns = storage_n(H, N) if N in SUPPORTED_HEAD_DIMS else N
-    if Ns == N:
-        return weights, factor1, factor2, N, 0
+    """(weights, tables, H, N, N_active) as the library takes them: narrow
+    heads zero-padded to storage_shape(H, N) (no gradient is taken here)."""
+    Hs, Ns = storage_shape(H, N)
+    if (Hs, Ns) == (H, N):
+        return weights, factor1, factor2, H, N, 0
     with torch.no_grad():
-        w, f1, f2 = _pad_heads(H, N, weights, factor1, factor2, Ns)
-    return w, f1, f2, Ns, N
+        w, f1, f2 = _pad_heads(H, N, weights, factor1, factor2, Ns, Hs)
+    return w, f1, f2, Hs, Ns, N if Ns != N else 0
 
 
 def _tables(factor1, factor2, rows: int):
@@ -86,7 +94,7 @@ def prefill(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, factor
     _validate(x, weights, factor1, factor2, H, N, eps, False)
     B, T, C = x.shape
     cache.check(B, H, N, x.device)
-    weights, factor1, factor2, N, n_active = _padded(H, N, weights, factor1, factor2)
+    weights, factor1, factor2, H, N, n_active = _padded(H, N, weights, factor1, factor2)
     Tc = cache.capacity
     if Tc < T:
         raise ValueError(f"cache capacity {Tc} is smaller than the prompt length {T}")
@@ -123,7 +131,7 @@ def decode_step(x, q_weight, k_weight, v_weight, g_weight, o_weight, factor1, fa
     B, _, C = x3.shape
     dev = x3.device
     cache.check(B, H, N, dev)
-    weights, factor1, factor2, N, n_active = _padded(H, N, weights, factor1, factor2)
+    weights, factor1, factor2, H, N, n_active = _padded(H, N, weights, factor1, factor2)
     return _decode_launch(x3, weights, factor1, factor2, H, N, n_active, pos, cache, eps, squeeze)
 
 
@@ -179,10 +187,10 @@ class DecodeGraph:
                   float(eps), False)
         cache.check(B, H, N, dev)
         # Padded once here, so the captured step allocates nothing.
-        weights, factor1, factor2, Nl, n_active = _padded(H, N, weights, factor1, factor2)
+        weights, factor1, factor2, Hl, Nl, n_active = _padded(H, N, weights, factor1, factor2)
         self._w = [w.contiguous() for w in weights]
         self._f1, self._f2 = _tables(factor1, factor2, cache.capacity)
-        self._args = (H, Nl, n_active)
+        self._args = (Hl, Nl, n_active)
         self._cache, self._eps = cache, float(eps)
         self.x = torch.zeros((B, C), device=dev, dtype=torch.bfloat16)
         self.pos = torch.zeros((B,), device=dev, dtype=torch.int32)
@@ -212,4 +220,5 @@ class DecodeGraph:
         return self.y
 
 
-__all__ = ["KVCache", "DecodeGraph", "prefill", "decode_step", "cache_width", "SUPPORTED_HEAD_DIMS", "MAX_C_FORWARD"]
+__all__ = ["KVCache", "DecodeGraph", "prefill", "decode_step", "cache_width", "cache_heads", "SUPPORTED_HEAD_DIMS",
+           "MAX_C_FORWARD"]

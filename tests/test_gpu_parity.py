@@ -139,8 +139,8 @@ BLOCK_CASES = [
     ("n32-h2-c640-b2-t129", _w("n32c", 2, 129, 640, 2, 32), None),
     ("n16-h4-c64-b2-t70", _w("n16", 2, 70, 64, 4, 16), None),
     ("n16-yarn4-h8-c128-b1-t333", _w("n16y", 1, 333, 128, 8, 16, 4.0, 64), None),
-    # C = H*N a multiple of 32 only (odd H with N = 32 or 16: zero-padded to
-    # 64; H = 2 with N = 16; a wide C whose last dx feature group holds 32
+    # C = H*N a multiple of 32 only (odd H with N = 32 or 16: one zero head
+    # added; H = 2 with N = 16; a wide C whose last dx feature group holds 32
     # features).
     ("n32-h3-c96-b2-t90", _w("n32h3", 2, 90, 96, 3, 32), None),
     ("n16-h2-c32-b2-t64", _w("n16h2", 2, 64, 32, 2, 16), None),

@@ -305,7 +305,8 @@ def test_static_decode_validation(lib):
 
 def test_descriptor_accepts_narrow_heads(lib):
     """32-wide heads run natively with an even H; heads of 16 dimensions are
-    described as N = 32 (or 64) with N_active, 32 with an odd H as N = 64."""
+    described as N = 32 (or 64) with N_active; 32 with an odd H as N = 64
+    (the Python API adds a zero head instead)."""
     for n_act in (0, 16, 32, 64):
         assert lib.mea_workspace_bytes(ctypes.byref(_d(N_active=n_act)), _lib.MEA_PASS_FWD) > 0
     for n_act in (0, 16, 32):
@@ -314,13 +315,14 @@ def test_descriptor_accepts_narrow_heads(lib):
 
 
 def test_storage_width_of_narrow_heads():
-    """storage_n: the head width the library runs for each (H, N)."""
-    from memory_efficient_attn_layer_amd.attention import storage_n
-    from memory_efficient_attn_layer_amd.decode import cache_width
+    """storage_shape: the (heads, head width) the library runs for each (H, N)."""
+    from memory_efficient_attn_layer_amd.attention import storage_shape
+    from memory_efficient_attn_layer_amd.decode import cache_heads, cache_width
 
-    assert [storage_n(4, n) for n in (16, 32, 64, 128, 256)] == [32, 32, 64, 128, 256]
-    assert [storage_n(3, n) for n in (16, 32, 64, 128, 256)] == [64, 64, 64, 128, 256]
-    assert cache_width(32, 8) == 32 and cache_width(16, 8) == 32 and cache_width(32, 5) == 64
+    assert [storage_shape(4, n) for n in (16, 32, 64, 128, 256)] == [(4, 32), (4, 32), (4, 64), (4, 128), (4, 256)]
+    assert [storage_shape(3, n) for n in (16, 32, 64, 128, 256)] == [(4, 32), (4, 32), (3, 64), (3, 128), (3, 256)]
+    assert cache_width(32, 8) == 32 and cache_width(16, 8) == 32 and cache_width(32, 5) == 32
+    assert cache_heads(32, 5) == 6 and cache_heads(16, 1) == 2 and cache_heads(64, 5) == 5
 
 
 def test_pad_heads_layout_and_gradients():
@@ -330,19 +332,21 @@ def test_pad_heads_layout_and_gradients():
     the caller's tensors as their slices."""
     from memory_efficient_attn_layer_amd.attention import _pad_heads
 
-    PAD_N = 64
+    PAD_N, PAD_H = 64, 4
     torch.manual_seed(0)
     H, N, C, T = 3, 32, 96, 10
     ws = [torch.randn(H * N, C, requires_grad=True) for _ in range(4)] + [torch.randn(C, H * N, requires_grad=True)]
     f1 = torch.randn(T, N, requires_grad=True)
     f2 = torch.randn(T, N, requires_grad=True)
-    (wq, wk, wv, wg, wo), p1, p2 = _pad_heads(H, N, ws, f1, f2, PAD_N)
-    assert wq.shape == (H * PAD_N, C) and wo.shape == (C, H * PAD_N) and p1.shape == (T, PAD_N)
+    (wq, wk, wv, wg, wo), p1, p2 = _pad_heads(H, N, ws, f1, f2, PAD_N, PAD_H)
+    assert wq.shape == (PAD_H * PAD_N, C) and wo.shape == (C, PAD_H * PAD_N) and p1.shape == (T, PAD_N)
     for h in range(H):
         assert torch.equal(wq[h * PAD_N:h * PAD_N + N], ws[0][h * N:(h + 1) * N])
         assert torch.count_nonzero(wq[h * PAD_N + N:(h + 1) * PAD_N]) == 0
         assert torch.equal(wo[:, h * PAD_N:h * PAD_N + N], ws[4][:, h * N:(h + 1) * N])
         assert torch.count_nonzero(wo[:, h * PAD_N + N:(h + 1) * PAD_N]) == 0
+    # The added head is zero throughout.
+    assert torch.count_nonzero(wq[H * PAD_N:]) == 0 and torch.count_nonzero(wo[:, H * PAD_N:]) == 0
     assert torch.equal(p1[:, :N], f1) and torch.all(p1[:, N:] == 1)
     assert torch.equal(p2[:, :N], f2) and torch.all(p2[:, N:] == 0)
     gq = torch.randn_like(wq)
@@ -351,8 +355,8 @@ def test_pad_heads_layout_and_gradients():
     (wq * gq).sum().backward()
     (wo * go).sum().backward()
     (p1 * g1).sum().backward()
-    assert torch.equal(ws[0].grad, gq.reshape(H, PAD_N, C)[:, :N].reshape(H * N, C))
-    assert torch.equal(ws[4].grad, go.reshape(C, H, PAD_N)[:, :, :N].reshape(C, H * N))
+    assert torch.equal(ws[0].grad, gq.reshape(PAD_H, PAD_N, C)[:H, :N].reshape(H * N, C))
+    assert torch.equal(ws[4].grad, go.reshape(C, PAD_H, PAD_N)[:, :H, :N].reshape(C, H * N))
     assert torch.equal(f1.grad, g1[:, :N])
 
 
