@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
     tok_row0 = (size_t)b * T;
   } else {
     const int nqb = (p.max_len + BQ - 1) / BQ;
-    const int lid = xcd_remap(blockIdx.x, p.nseq * nh * nqb);
+    const int lid = attn_item(blockIdx.x, p.nseq * nh * nqb, nqb, N <= 64 ? 3 : 1);
     const int bh = lid / nqb;
     qi = nqb - 1 - lid % nqb;
     b = bh / nh;
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
     tok_row0 = (size_t)b * T;
   } else {
     const int nkb = (p.max_len + BKV - 1) / BKV;
-    const int lid = xcd_remap(blockIdx.x, p.nseq * nh * nkb);
+    const int lid = attn_item(blockIdx.x, p.nseq * nh * nkb, nkb, N <= 64 ? 3 : 1);
     const int bh = lid / nkb;
     ki = lid % nkb;
     b = bh / nh;

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256, N <= 64 ? 4 : N == 128 ? 3 : 1) void attn_fwd_
     tok_row0 = (size_t)b * T;
   } else {
     const int nqb = (p.max_len + BQ - 1) / BQ;
-    const int lid = xcd_remap(blockIdx.x, p.nseq * p.H * nqb);
+    const int lid = attn_item(blockIdx.x, p.nseq * p.H * nqb, nqb, N <= 64 ? 3 : 1);
     bh = lid / nqb;  // sequence-major (s, h)
     qi = nqb - 1 - lid % nqb;
     b = bh / p.H;

@@ -295,6 +295,10 @@ constexpr int kTailHeads = 4;
 // all three kernels; four in the forward, its occupancy, gained 0.2%); the
 // step -0.5 to -1.3%. With 128-wide heads (two slots) dK/dV ran 1.1% slower
 // and T = 32768 was unchanged, so only N <= 64 uses it (slots = 1: plain).
+// Packed sequences take the same order over their (sequence, head, block)
+// items, blocks past a sequence's end exiting at once (64 sequences of 1024
+// to 4096 tokens, against plain per-XCD ranges: dK/dV -4.2%, dQ -2.2%,
+// forward -2.7%, the step -1.7%).
 constexpr int kCusPerXcd = 32;
 // (Host and device: tests/work_order.cpp checks on the CPU that it is a
 // permutation of 0 .. G - 1.)
