@@ -137,6 +137,8 @@ BLOCK_CASES = [
     ("n32-yarn4-h6-c192-b1-t300", _w("n32y", 1, 300, 192, 6, 32, 4.0, 128), None),
     ("n32-h16-c512-b1-t700", _w("n32l", 1, 700, 512, 16, 32), None),
     ("n32-h2-c640-b2-t129", _w("n32c", 2, 129, 640, 2, 32), None),
+    ("n32-t1-h4-c128-b3", _w("n32t1", 3, 1, 128, 4, 32), None),
+    ("n32-ragged-h2-c64-b3-t77", _w("n32r", 3, 77, 64, 2, 32), None),
     ("n16-h4-c64-b2-t70", _w("n16", 2, 70, 64, 4, 16), None),
     ("n16-yarn4-h8-c128-b1-t333", _w("n16y", 1, 333, 128, 8, 16, 4.0, 64), None),
     # C = H*N a multiple of 32 only (odd H with N = 32 or 16: one zero head
@@ -167,7 +169,8 @@ def test_block_forward_backward(label, w, B):
 BUFFER_TABLE_CASES = [c for c in BLOCK_CASES if c[0] in {
     "cfg0-full", "cfg1-b1-t4096", "cfg2-yarn4-b1-t2048", "cfg3-b1-t1024", "ragged-b3-t77", "ragged-b2-t200-n128",
     "t129-b1", "yarn8-b2-t300-n128", "h5-hn320-b1-t150", "c2048-h16-n128-yarn8-b1-t256", "n32-h8-c256-b2-t100",
-    "n16-h4-c64-b2-t70", "n256-h2-c512-b2-t130", "n256-yarn4-h3-c768-b1-t200", "n256-h1-c256-b1-t70"}]
+    "n16-h4-c64-b2-t70", "n256-h2-c512-b2-t130", "n256-yarn4-h3-c768-b1-t200", "n256-h1-c256-b1-t70",
+    "n32-h16-c512-b1-t700", "n32-h3-c96-b2-t90"}]
 
 
 @pytest.mark.parametrize("label,w,B", BUFFER_TABLE_CASES, ids=[c[0] for c in BUFFER_TABLE_CASES])
