@@ -35,7 +35,7 @@ METRIC = "fwd+bwd tokens/s & peak mem, attn block bf16 B64 T4096 C512 H8 N64"
 
 
 def metric_of(w) -> str:
-    """The metric string of a workload (the north-star one for workload 1)."""
+    """The metric string of a workload (the headline one, B64 T4096 C512 H8 N64, for workload 1)."""
     kind = "fwd+bwd" if w.backward else "fwd (prefill, no grad)"
     return f"{kind} tokens/s & peak mem, attn block bf16 B{w.B} T{w.T} C{w.C} H{w.H} N{w.N}"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
@@ -219,7 +219,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", type=int, default=1, help="workload id (1 = the north-star shape)")
+    ap.add_argument("--workload", type=int, default=1, help="workload id (1 = the headline shape, B64 T4096 C512 H8 N64)")
     ap.add_argument("--no-eager", action="store_true",
                     help="skip the eager checkpoint+SDPA comparator (timed and peak HBM on the same GPU)")
     ap.add_argument("--table-grad", action="store_true",
@@ -319,7 +319,7 @@ def main():
     avg_s = prof[dom][1] / prof[dom][0] * 1e-3
     achieved = work[dom]["flops"] / avg_s / 1e12
     # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE runs,
-    # which cover the north-star workload only.
+    # which cover the headline workload (B64 T4096 C512 H8 N64) only.
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if w.wid == 1 and tfile.exists():
