@@ -7,7 +7,8 @@
 //
 // The product is computed transposed, D^T = W x^T: the A operand is a slice
 // of the stacked weights of one head h (features; [Wq_h; Wv_h; Wk_h; Wg_h]
-// for N = 64, [Wq_h; Wk_h] and [Wv_h; Wg_h] tiles for N = 128), the B
+// for N = 64, [Wq_h; Wk_h] and [Wv_h; Wg_h] tiles for N = 128; for N = 32
+// the same four of a head pair, [Wq; Wv; Wk; Wg] rows 64h .. 64h + 63), the B
 // operand a tile of x rows (tokens). In the 16x16 accumulator layout a
 // lane then holds one token and 4 consecutive features, so the head RMSNorm
 // is an in-lane sum plus two lane exchanges, both members of every rotary
