@@ -149,19 +149,23 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // 32 consecutive queries whose q and dO rows stay in registers as the B
 // operands of
 //   S^T = K Q^T   and   dP^T = V dO^T      (A = K, V rows from LDS)
-// on v_mfma_f32_32x32x16_bf16. The query index sits on the lane, so the row
-// statistics ride along as one more k-block of those products (stored q is
-// in log2 units): with -lse*log2e and -delta split into exact bf16 terms on
-// the query side and (1, 1, 1) selectors on the key side, the accumulators
-// come out as log2 P and dP - delta, and dS^T = P^T (dP^T - delta) is one
-// exp2 and one multiply per score, already the B operand (k = key) of
+// on v_mfma_f32_32x32x16_bf16. The query index sits on the lane, and the
+// accumulators start from the lane's row statistics (stored q is in log2
+// units): -lse*log2e for S^T and -delta for dP^T, four copies of each per
+// query in a wave-private LDS area, read straight into the accumulator
+// registers (four 16-byte reads per product). They come out as log2 P and
+// dP - delta, and dS^T = P^T (dP^T - delta) is one exp2 and one multiply per
+// score, already the B operand (k = key) of
 //   dQ^T += K^T dS^T
 // whose A operand K^T is read from the row-major K tile with the transposing
 // ds_read_b64_tr_b16. Key tiles of 64 stream through LDS (global_load_lds,
 // double-buffered, one barrier per tile); tiles wholly below a wave's first
 // query run in a branch-free loop, the rest of the diagonal region after it.
-// For N = 64 three workgroups share a CU (164 registers): 64 queries per wave
+// For N = 64 three workgroups share a CU (160 registers): 64 queries per wave
 // (two blocks sharing every K/V fragment) held two per SIMD ran 4.4% slower.
+// (The statistics were earlier added by one more MFMA k-block per product,
+// their exact bf16 terms against (1, 1, 1) selectors; the LDS start values
+// save those MFMAs: dQ -0.9%, dK/dV -3%.)
 // ---------------------------------------------------------------------------
 template <int N, bool VARLEN>
 __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
   constexpr int LOADS = TILE / 8 / 256;
   constexpr int FP = N + 4;  // fp32 staging pitch
   constexpr int SM_LOOP = 4 * TILE * 2;  // bytes: [stage][K | V]
-  constexpr int SM_STAT = 4 * QB * 64 * 16;  // bytes: statistic k-blocks, [wave][qb][lane]
+  constexpr int SM_STAT = 4 * QB * 2 * 4 * 32 * 16;  // bytes: [wave][qb][lse | delta][copy][query] x 4
   constexpr int SM_OUT = 4 * QW * FP * 4;
   constexpr int SMEM = SM_LOOP + SM_STAT > SM_OUT ? SM_LOOP + SM_STAT : SM_OUT;
   __shared__ __attribute__((aligned(16))) unsigned char smem_raw[SMEM];
@@ -224,14 +228,15 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
     const bf16_bits* kg = p.k + head_off;
     const bf16_bits* vg = p.v + head_off;
 
-    // q^T and dO^T fragments (B operands), and the statistic k-block of the
-    // lane's query q0w + 32qb + c: (-lse*log2e, -delta) in elements 0..5 of the
-    // lanes with h == 0 (zero in the others), kept in a wave-private LDS area
-    // the loop does not touch and matched by the selectors sel_s (S) and sel_d
-    // (dP). The selectors may be the same in every lane, which keeps them
-    // plain constants.
+    // q^T and dO^T fragments (B operands), and the start values of the S^T
+    // and dP^T accumulators of the lane's query q0w + 32qb + c: -lse*log2e
+    // (written by the lanes with h == 0) and -delta (h == 1), each as four
+    // copies of a 16-byte row [qb][lse | delta][copy][query], in a
+    // wave-private LDS area the loop does not touch. Four distinct copies keep
+    // the four reads that fill an accumulator from being merged into one read
+    // and twelve register moves.
     bf16x8 qf[QB][KS], df[QB][KS];
-    u32x4* stat = reinterpret_cast<u32x4*>(smem_raw + SM_LOOP) + wave * QB * 64;
+    f32x4* statq = reinterpret_cast<f32x4*>(smem_raw + SM_LOOP) + wave * QB * 256;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int t = min(q0w + 32 * qb + c, T - 1);
@@ -241,10 +246,10 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
         qf[qb][ks] = as_frag(ld16(p.q + off));
         df[qb][ks] = as_frag(ld16(p.dO + off));
       }
-      const u32x4 sw = stat_pack(-p.lse[head_row0 + t] * kLog2e, -p.delta[head_row0 + t]);
-      stat[qb * 64 + lane] = h == 0 ? sw : u32x4{0u, 0u, 0u, 0u};
+      const float sv = h == 0 ? -p.lse[head_row0 + t] * kLog2e : -p.delta[head_row0 + t];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) statq[qb * 256 + h * 128 + j * 32 + c] = f32x4{sv, sv, sv, sv};
     }
-    const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
 
     auto issue_tile = [&](int j0, int stage) {
       bf16_bits* kt = smem + stage * 2 * TILE;
@@ -296,8 +301,16 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
           sf[qb][0] = sf[qb][1] = as_frag(u32x4{0u, 0u, 0u, 0u});
           continue;
         }
-        const bf16x8 stf = as_frag(stat[qb * 64 + lane]);
-        f32x16 s = mfma32(sel_s, stf, zero16()), dp = mfma32(sel_d, stf, zero16());
+        f32x16 s, dp;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 a = statq[qb * 256 + j * 32 + c], b = statq[qb * 256 + 128 + j * 32 + c];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s[4 * j + e] = a[e];
+            dp[4 * j + e] = b[e];
+          }
+        }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           s = mfma32(kf[ks], qf[qb][ks], s);
@@ -397,10 +410,10 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
 // consecutive keys whose K rows stay in registers and whose V rows sit in a
 // per-wave LDS block laid out as the lane's fragments, as the B operands of
 //   S  = Q K^T   and   dP = dO V^T        (A = Q, dO rows from LDS)
-// on v_mfma_f32_32x32x16_bf16, each with one more k-block that subtracts
-// the query statistics (stored q is in log2 units): -lse*log2e and -delta,
-// split into exact bf16 terms per query tile when its statistics are
-// published, on the query side, and (1, 1, 1) selectors on the key side. The
+// on v_mfma_f32_32x32x16_bf16, whose accumulators start from the query
+// statistics (stored q is in log2 units): -lse*log2e and -delta of each
+// query tile sit in LDS as fp32 rows, and a lane's 16 accumulator elements
+// (queries 8j + 4h + 0..3, j = 0..3) are four 16-byte reads of each row. The
 // accumulators come out as log2 P and dP - delta. The key index sits on the
 // lane, so P and dS = P (dP - delta) are already the B operands (k = query) of
 //   dV^T += dO^T P   and   dK^T += Q^T dS
@@ -429,15 +442,15 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
   constexpr int TILE = BQ * N;
   constexpr int LOADS = TILE / 8 / 256;
   constexpr int FP = N + 4;  // fp32 staging pitch
-  constexpr int SM_LOOP = 2 * 2 * TILE * 2 + 2 * (BQ + 1) * 16;  // bytes
+  constexpr int SM_LOOP = 2 * 2 * TILE * 2 + 2 * 2 * BQ * 4;  // bytes
   constexpr int SM_V = 4 * KS * 64 * 16;  // bytes: each wave's V^T fragments, [wave][ks][lane]
   constexpr int SM_OUT = 4 * 32 * FP * 4;
   constexpr int SMEM = SM_LOOP + SM_V > SM_OUT ? SM_LOOP + SM_V : SM_OUT;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
   bf16_bits* tiles = reinterpret_cast<bf16_bits*>(smem);           // [stage][Q | dO]
-  // [stage][query]: statistic k-block words of each query of the tile, then
-  // one zero block read by the lanes that hold k-elements 8..15.
-  u32x4* stats = reinterpret_cast<u32x4*>(smem + 2 * 2 * TILE * 2);
+  // [stage][-lse*log2e | -delta][query]: the accumulator start values of the
+  // tile's queries.
+  float* statf = reinterpret_cast<float*>(smem + 2 * 2 * TILE * 2);
   u32x4* vown = reinterpret_cast<u32x4*>(smem + SM_LOOP);
 
   // Each XCD walks whole heads, the key block that sees the most queries
@@ -496,7 +509,6 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
     }
 
     float st_l = 0.f, st_d = 0.f;
-    if (tid < 2) stats[tid * (BQ + 1) + BQ] = u32x4{0u, 0u, 0u, 0u};
     auto issue_tile = [&](int q0, int stage) {
       bf16_bits* qt = tiles + stage * 2 * TILE;
 #pragma unroll
@@ -504,8 +516,11 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
         const int slot = (u * 4 + wave) * 64 + lane;
         const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
         const size_t off = (size_t)min(q0 + row, T - 1) * N + cc * 8;
-        g2lds16(qg + off, qt + (u * 4 + wave) * 512);
-        g2lds16(dg + off, qt + TILE + (u * 4 + wave) * 512);
+        // The LDS destination from a uniform wave index: held in a vector
+        // register instead, it spilled from the main loop.
+        const int wu = __builtin_amdgcn_readfirstlane(wave);
+        g2lds16(qg + off, qt + (u * 4 + wu) * 512);
+        g2lds16(dg + off, qt + TILE + (u * 4 + wu) * 512);
       }
       if (tid < BQ) {
         const size_t t = head_row0 + min(q0 + tid, T - 1);
@@ -516,7 +531,10 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
     // Called after wait_vmcnt0(): st_l / st_d are consumed only once every load
     // of the tile has landed, so no wait is placed inside the prefetch.
     auto publish_stats = [&](int stage) {
-      if (tid < BQ) stats[stage * (BQ + 1) + tid] = stat_pack(-st_l * kLog2e, -st_d);
+      if (tid < BQ) {
+        statf[stage * 2 * BQ + tid] = -st_l * kLog2e;
+        statf[stage * 2 * BQ + BQ + tid] = -st_d;
+      }
     };
 
     f32x16 dv[KB][DB], dk[KB][DB];
@@ -534,9 +552,6 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
     // workgroups per CU.)
     auto kofs = [&](int ks) { return swz_off<CH>(c, 16 * ks + 8 * h); };
     auto tofs = [&](int x, int db) { return swz_off<CH>(tr_row + 8 * x, 32 * db + tr_col); };
-    // Key-side selectors of the statistic k-block (the same in every lane: the
-    // query side is zero in the lanes holding k-elements 8..15).
-    const bf16x8 sel_s = as_frag(stat_sel_a(true)), sel_d = as_frag(stat_sel_b(true));
 
     // Query tiles are walked from the last one down: every workgroup of a
     // head then reads the same tile at about the same time (walking up from
@@ -553,7 +568,7 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
       if (it + 1 < nq) issue_tile(q0 - BQ, (it + 1) & 1);
       const bf16_bits* qt = tiles + (it & 1) * 2 * TILE;
       const bf16_bits* dt = qt + TILE;
-      const u32x4* sts = stats + (it & 1) * (BQ + 1);
+      const float* stf = statf + (it & 1) * 2 * BQ;
       // One 32-query step in three parts: S and dP (MFMA), P and dS (exp2,
       // multiply, convert; DIAG steps also mask key > query and query >= T),
       // then the dV and dK updates (MFMA).
@@ -562,10 +577,18 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
         bf16x8 pb[2], sb[2];
       };
       auto sdp = [&](int sub, Sub& u) {
-        // Statistic k-block of the lane's query row qs0 + c (zero for h == 1).
-        const bf16x8 sa = as_frag(sts[h == 0 ? 32 * sub + c : BQ]);
-        u.s = mfma32(sa, sel_s, zero16());
-        u.dp = mfma32(sa, sel_d, zero16());
+        // Start values: element 4j + e holds query qs0 + 8j + 4h + e.
+        const float* sl = stf + 32 * sub + 4 * h;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(sl + 8 * j);
+          const f32x4 b = *reinterpret_cast<const f32x4*>(sl + BQ + 8 * j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            u.s[4 * j + e] = a[e];
+            u.dp[4 * j + e] = b[e];
+          }
+        }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const bf16x8 qa = as_frag(*reinterpret_cast<const u32x4*>(qt + 32 * sub * N + kofs(ks)));

@@ -185,34 +185,6 @@ __device__ __forceinline__ float fast_sigmoid(float a) {
   return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-a * kLog2e));
 }
 
-// Statistic columns for an MFMA reduction: a per-row fp32 value x is added
-// to a product by appending k-elements (x_hi, x_mid, x_lo) on one side and
-// (1, 1, 1) on the other. The three bf16 terms take successive 8-bit pieces
-// of the significand (round to nearest each time), so x_hi + x_mid + x_lo == x
-// exactly and the MFMA's fp32 accumulation adds x itself. stat_pack puts the
-// terms of a (elements 0..2) and b (elements 3..5) into the first three
-// 32-bit words of a k-block.
-__device__ __forceinline__ void split3(float x, uint32_t& e0, uint32_t& e1, uint32_t& e2) {
-  e0 = f2bf(x);
-  const float r1 = x - bf2f((bf16_bits)e0);
-  e1 = f2bf(r1);
-  e2 = f2bf(r1 - bf2f((bf16_bits)e1));
-}
-__device__ __forceinline__ u32x4 stat_pack(float a, float b) {
-  uint32_t a0, a1, a2, b0, b1, b2;
-  split3(a, a0, a1, a2);
-  split3(b, b0, b1, b2);
-  return u32x4{a0 | (a1 << 16), a2 | (b0 << 16), b1 | (b2 << 16), 0u};
-}
-// The matching (1, 1, 1) selectors, for k-block lanes that hold elements
-// 0..7 (the other lanes pass zero): element 0..2 (first) or 3..5 (second).
-__device__ __forceinline__ u32x4 stat_sel_a(bool on) {
-  return on ? u32x4{0x3F803F80u, 0x00003F80u, 0u, 0u} : u32x4{0u, 0u, 0u, 0u};
-}
-__device__ __forceinline__ u32x4 stat_sel_b(bool on) {
-  return on ? u32x4{0u, 0x3F800000u, 0x3F803F80u, 0u} : u32x4{0u, 0u, 0u, 0u};
-}
-
 // Row-major bf16 tiles in LDS are stored as 16-byte chunks; chunk c of row r
 // sits at chunk slot c ^ swz(r). Two access patterns must be conflict-free:
 //  - 16-byte row reads: 16 lanes read one chunk of 16 consecutive rows. For
