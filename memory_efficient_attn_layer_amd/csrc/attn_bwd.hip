@@ -246,7 +246,9 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
         qf[qb][ks] = as_frag(ld16(p.q + off));
         df[qb][ks] = as_frag(ld16(p.dO + off));
       }
-      const float sv = h == 0 ? -p.lse[head_row0 + t] * kLog2e : -p.delta[head_row0 + t];
+      // One load per lane (a selected pointer, not two loads under a branch).
+      const float sl = (h == 0 ? p.lse : p.delta)[head_row0 + t];
+      const float sv = h == 0 ? -sl * kLog2e : -sl;
 #pragma unroll
       for (int j = 0; j < 4; ++j) statq[qb * 256 + h * 128 + j * 32 + c] = f32x4{sv, sv, sv, sv};
     }
