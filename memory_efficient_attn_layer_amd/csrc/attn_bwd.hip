@@ -565,7 +565,11 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
     wait_vmcnt0();
     publish_stats(0);
     __syncthreads();
-    for (int it = 0; it < nq; ++it) {
+    // One query tile. MASKED: the tile may touch the causal diagonal or the
+    // sequence end (per-step tests and masks); the tiles between hold only
+    // full steps for every wave and run without any test.
+    auto tile = [&](int it, auto masked_tag) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
       const int q0 = k0 + (nq - 1 - it) * BQ;
       if (it + 1 < nq) issue_tile(q0 - BQ, (it + 1) & 1);
       const bf16_bits* qt = tiles + (it & 1) * 2 * TILE;
@@ -641,19 +645,29 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
 #pragma unroll
       for (int sub = 0; sub < BQ / 32; ++sub) {
         const int qs0 = q0 + 32 * sub;
-        if (qs0 + 31 < kw0 || qs0 >= T) continue;  // wave-uniform: nothing to add
+        if (MASKED && (qs0 + 31 < kw0 || qs0 >= T)) continue;  // wave-uniform: nothing to add
         Sub u;
         sdp(sub, u);
-        if (qs0 < kw0 + KW - 1 || qs0 + 31 >= T)
+        if (MASKED && (qs0 < kw0 + KW - 1 || qs0 + 31 >= T))
           soft(sub, u, std::true_type{});
         else
           soft(sub, u, std::false_type{});
         kv(sub, u);
+        // Keeps the next step's S and dP from being scheduled into this one
+        // (their registers would not fit beside this step's).
+        if (!MASKED) __builtin_amdgcn_sched_barrier(0);
       }
       wait_vmcnt0();
       if (it + 1 < nq) publish_stats((it + 1) & 1);
       __syncthreads();
-    }
+    };
+    // Tiles it < nfull lie wholly above the block's keys (q0 >= k0 + BKV);
+    // the first one (the highest queries) may run past the sequence end.
+    const int nfull = nq - BKV / BQ;
+    int it = 0;
+    if (nfull > 0 && (T - k0) % BQ != 0) tile(it++, std::true_type{});
+    for (; it < nfull; ++it) tile(it, std::false_type{});
+    for (; it < nq; ++it) tile(it, std::true_type{});
 
     // Epilogue per 32-key block: stage dV (then dK * scale) as fp32 rows and run
     // the row-wise tails (rx scale; k RMSNorm + rotary backward for dK).
