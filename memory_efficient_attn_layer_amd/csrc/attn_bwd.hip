@@ -253,15 +253,37 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 256 ? 1 : 2) void attn_bwd_
       for (int j = 0; j < 4; ++j) statq[qb * 256 + h * 128 + j * 32 + c] = f32x4{sv, sv, sv, sv};
     }
 
-    auto issue_tile = [&](int j0, int stage) {
-      bf16_bits* kt = smem + stage * 2 * TILE;
+    // Tile loads: lane L of load u fills 16-byte slot L of row block u*4+wave;
+    // its row and swizzled chunk are fixed, so a whole tile is fetched from a
+    // wave-uniform base (row j0) plus a lane-constant byte offset, and only a
+    // tile that runs past the sequence end takes per-lane clamped addresses.
+    uint32_t ld_off[LOADS];
 #pragma unroll
-      for (int u = 0; u < LOADS; ++u) {
-        const int slot = (u * 4 + wave) * 64 + lane;
-        const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
-        const size_t off = (size_t)min(j0 + row, T - 1) * N + cc * 8;
-        g2lds16(kg + off, kt + (u * 4 + wave) * 512);
-        g2lds16(vg + off, kt + TILE + (u * 4 + wave) * 512);
+    for (int u = 0; u < LOADS; ++u) {
+      const int slot = (u * 4 + wave) * 64 + lane;
+      const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+      ld_off[u] = (uint32_t)(row * N + cc * 8) * 2u;
+    }
+    const uint32_t smem_b = lds_addr(smem);
+    auto issue_tile = [&](int j0, int stage) {
+      const uint32_t kt = smem_b + (uint32_t)(stage * 2 * TILE) * 2u;
+      if (j0 + BKV <= T) {
+        const bf16_bits* kb = kg + (size_t)j0 * N;
+        const bf16_bits* vb = vg + (size_t)j0 * N;
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+          g2lds16_s(kb, ld_off[u], kt + (uint32_t)(u * 4 + wave) * 1024u);
+          g2lds16_s(vb, ld_off[u], kt + (uint32_t)(TILE * 2) + (uint32_t)(u * 4 + wave) * 1024u);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+          const int slot = (u * 4 + wave) * 64 + lane;
+          const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+          const size_t off = (size_t)min(j0 + row, T - 1) * N + cc * 8;
+          g2lds16(kg + off, kt + (uint32_t)(u * 4 + wave) * 1024u);
+          g2lds16(vg + off, kt + (uint32_t)(TILE * 2) + (uint32_t)(u * 4 + wave) * 1024u);
+        }
       }
     };
 
@@ -511,18 +533,38 @@ __global__ __launch_bounds__(256, N <= 64 ? 3 : N == 128 ? 2 : 1) void attn_bwd_
     }
 
     float st_l = 0.f, st_d = 0.f;
-    auto issue_tile = [&](int q0, int stage) {
-      bf16_bits* qt = tiles + stage * 2 * TILE;
+    // Tile loads as in the dQ kernel: a whole tile from a uniform base plus a
+    // lane-constant byte offset, a tile past the sequence end clamped per
+    // lane. The LDS destination comes from a uniform wave index: held in a
+    // vector register instead, it spilled from the main loop.
+    uint32_t ld_off[LOADS];
 #pragma unroll
-      for (int u = 0; u < LOADS; ++u) {
-        const int slot = (u * 4 + wave) * 64 + lane;
-        const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
-        const size_t off = (size_t)min(q0 + row, T - 1) * N + cc * 8;
-        // The LDS destination from a uniform wave index: held in a vector
-        // register instead, it spilled from the main loop.
-        const int wu = __builtin_amdgcn_readfirstlane(wave);
-        g2lds16(qg + off, qt + (u * 4 + wu) * 512);
-        g2lds16(dg + off, qt + TILE + (u * 4 + wu) * 512);
+    for (int u = 0; u < LOADS; ++u) {
+      const int slot = (u * 4 + wave) * 64 + lane;
+      const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+      ld_off[u] = (uint32_t)(row * N + cc * 8) * 2u;
+    }
+    const uint32_t tiles_b = lds_addr(tiles);
+    auto issue_tile = [&](int q0, int stage) {
+      const uint32_t qt = tiles_b + (uint32_t)(stage * 2 * TILE) * 2u;
+      const int wu = __builtin_amdgcn_readfirstlane(wave);
+      if (q0 + BQ <= T) {
+        const bf16_bits* qb = qg + (size_t)q0 * N;
+        const bf16_bits* db = dg + (size_t)q0 * N;
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+          g2lds16_s(qb, ld_off[u], qt + (uint32_t)(u * 4 + wu) * 1024u);
+          g2lds16_s(db, ld_off[u], qt + (uint32_t)(TILE * 2) + (uint32_t)(u * 4 + wu) * 1024u);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+          const int slot = (u * 4 + wave) * 64 + lane;
+          const int row = slot / CH, cc = (slot % CH) ^ chunk_swz<CH>(row);
+          const size_t off = (size_t)min(q0 + row, T - 1) * N + cc * 8;
+          g2lds16(qg + off, qt + (uint32_t)(u * 4 + wu) * 1024u);
+          g2lds16(dg + off, qt + (uint32_t)(TILE * 2) + (uint32_t)(u * 4 + wu) * 1024u);
+        }
       }
       if (tid < BQ) {
         const size_t t = head_row0 + min(q0 + tid, T - 1);
