@@ -161,7 +161,7 @@ __device__ __forceinline__ void head_row_bwd(const float* stg, int FP, int t0, c
 // ds_read_b64_tr_b16. Key tiles of 64 stream through LDS (global_load_lds,
 // double-buffered, one barrier per tile); tiles wholly below a wave's first
 // query run in a branch-free loop, the rest of the diagonal region after it.
-// For N = 64 three workgroups share a CU (160 registers): 64 queries per wave
+// For N = 64 three workgroups share a CU (163 registers): 64 queries per wave
 // (two blocks sharing every K/V fragment) held two per SIMD ran 4.4% slower.
 // (The statistics were earlier added by one more MFMA k-block per product,
 // their exact bf16 terms against (1, 1, 1) selectors; the LDS start values
