@@ -347,12 +347,17 @@ const char* mea_strerror(int code);
  *   mea_profile_enable(0)  stops recording (records are kept);
  *   mea_profile_read(k, &count, &total_ms) waits for the recorded events of
  *     kernel k and returns its launch count and summed duration;
- *   mea_profile_kernel_name(k) names kernel k, NULL past the last one.
+ *   mea_profile_kernel_name(k) names kernel k, NULL past the last one;
+ *   mea_profile_select(k) limits recording to kernel k (its launches alone
+ *     are bracketed; each event pair adds about 8 us of queue time, so a
+ *     caller timing a whole step can keep the other launches bare), k = -1
+ *     (the initial state) records every kernel. MEA_ERR_NULL for any other k.
  * Recording is process-wide and serialised by a mutex.
  */
 int mea_profile_enable(int on);
 int mea_profile_read(int kernel, int* count, double* total_ms);
 const char* mea_profile_kernel_name(int kernel);
+int mea_profile_select(int kernel);
 
 /* Library version string. */
 const char* mea_version(void);

@@ -75,6 +75,7 @@ EXPORTS = {
     "mea_profile_enable": (ctypes.c_int, [ctypes.c_int]),
     "mea_profile_read": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_double)]),
     "mea_profile_kernel_name": (ctypes.c_char_p, [ctypes.c_int]),
+    "mea_profile_select": (ctypes.c_int, [ctypes.c_int]),
 }
 
 _lock = threading.Lock()
@@ -141,6 +142,22 @@ def stream_of(device: torch.device) -> int:
 
 def profile_enable(on: bool) -> None:
     check(load().mea_profile_enable(1 if on else 0), "mea_profile_enable")
+
+
+def profile_select(name: str | None) -> None:
+    """Limits the recording to the named kernel (None: every kernel)."""
+    lib = load()
+    k = -1
+    if name is not None:
+        k = 0
+        while True:
+            n = lib.mea_profile_kernel_name(k)
+            if n is None:
+                raise ValueError(f"no kernel named {name!r}")
+            if n.decode() == name:
+                break
+            k += 1
+    check(lib.mea_profile_select(k), "mea_profile_select")
 
 
 def profile_read() -> dict:

@@ -172,6 +172,7 @@ struct ProfRec {
 };
 std::mutex g_prof_mu;
 bool g_prof_on = false;
+int g_prof_only = -1;  // record only this kernel (-1: all)
 std::vector<ProfRec> g_prof;
 std::vector<hipEvent_t> g_pool;
 
@@ -191,7 +192,7 @@ hipEvent_t pool_event() {
 template <class F>
 hipError_t timed(int kernel, hipStream_t s, F launch) {
   std::unique_lock<std::mutex> lk(g_prof_mu);
-  if (!g_prof_on) {
+  if (!g_prof_on || (g_prof_only >= 0 && kernel != g_prof_only)) {
     lk.unlock();
     return launch();
   }
@@ -983,6 +984,13 @@ int mea_profile_read(int kernel, int* count, double* total_ms) {
 
 const char* mea_profile_kernel_name(int kernel) {
   return kernel >= 0 && kernel < K_COUNT ? kKernelNames[kernel] : nullptr;
+}
+
+int mea_profile_select(int kernel) {
+  if (kernel < -1 || kernel >= K_COUNT) return MEA_ERR_NULL;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_only = kernel;
+  return MEA_OK;
 }
 
 }  // extern "C"

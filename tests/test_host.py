@@ -51,6 +51,24 @@ def test_strerror_and_version(lib):
     assert lib.mea_version().decode().startswith("mea ")
 
 
+def test_profile_select_bounds(lib):
+    """mea_profile_select takes -1 (every kernel) or a kernel id; the
+    selection is host state only (no GPU call)."""
+    n = 0
+    while lib.mea_profile_kernel_name(n) is not None:
+        n += 1
+    err = _header_enum("MEA_ERR_NULL")
+    assert lib.mea_profile_select(-2) == err
+    assert lib.mea_profile_select(n) == err
+    for k in (-1, 0, n - 1):
+        assert lib.mea_profile_select(k) == 0
+    lib.mea_profile_select(-1)
+    _lib.profile_select("attn_bwd_dkdv")
+    _lib.profile_select(None)
+    with pytest.raises(ValueError):
+        _lib.profile_select("no_such_kernel")
+
+
 def _d(B=2, T=256, C=256, H=4, N=64, T_max=None, eps=1e-6, N_active=0):
     return _lib.desc(B, T, C, H, N, T if T_max is None else T_max, eps, N_active)
 
