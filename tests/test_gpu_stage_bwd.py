@@ -67,6 +67,8 @@ CASES = [
     ("yarn8-b2-t300-n128", _w("y8", 2, 300, 256, 2, 128, 8.0, 64), None),
     ("h5-hn320-b1-t150", _w("h5", 1, 150, 256, 5, 64), None),
     ("n32-yarn4-b2-t300", _w("n32", 2, 300, 256, 8, 32, 4.0, 128), None),
+    ("n256-b2-t40", _w("n256", 2, 40, 256, 2, 256), None),
+    ("n256-b1-t2", _w("n256t2", 1, 2, 256, 2, 256), None),
 ]
 
 
